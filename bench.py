@@ -1,0 +1,304 @@
+"""Benchmark of the MI355X quantised DiT hot path (one JSON line on stdout).
+
+Headline (``value``): BASELINE cfg 1 -- fused QKV split + per-head q/k RMSNorm +
+3-D RoPE + 4-slot KV-ring write over L=10800 tokens, 40x128 heads, in GB/s of
+algorithmic HBM traffic. One step = one launch over the whole chunk, inputs
+resident in HBM. Also reported in the same line: the cfg 2 FP8 GEMM sweep at
+M=10800 (TFLOP/s, fraction of dense FP8 MFMA peak), the cfg 3 small-M GEMMs
+(GB/s) and the activation quantiser (GB/s), each timed with HIP events on the
+launch stream, plus the reference's CPU torch path timed on the host cores on a
+bounded sample (``cpu_baseline``).
+
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu] [--only qkv|gemm|...]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "joyai-video-edit_amd"))
+sys.path.insert(0, ROOT)
+
+METRIC = "FP8 GEMM TFLOP/s (% fp8 MFMA peak); QKV-norm-RoPE GB/s (% HBM peak)"
+PEAK_HBM_GBS = 8000.0         # MI355X HBM3E, AMD published
+PEAK_FP8_TFLOPS = 5000.0      # MI355X dense FP8 MFMA, AMD published (no sparsity)
+
+L_TOK, HEADS, HEAD_DIM = 10800, 40, 128
+E = HEADS * HEAD_DIM
+RING_SLOTS, SLOT = 4, 1
+GEMM_SHAPES = [("qkv", 5120, 15360), ("out_proj", 5120, 5120), ("ffn_up", 5120, 13824),
+               ("ffn_down", 13824, 5120)]
+SMALL_M = [64, 256, 512]
+
+
+def qkv_bytes(L: int) -> int:
+    """Algorithmic bytes of one fused launch: read q,k,v (bf16) + cos/sin half tables +
+    q/k weights; write q_rope, k_rope, k_pre -> cache, v -> cache."""
+    return 3 * L * E * 2 + L * (HEAD_DIM // 2) * 2 * 2 + 2 * HEAD_DIM * 2 + 4 * L * E * 2
+
+
+def gemm_bytes(M, N, K) -> int:
+    return M * K + K * N + 2 * M * N + 4 * M + 4 * N + 2 * N
+
+
+def quant_bytes(M, K) -> int:
+    return 2 * M * K + M * K + 4 * M
+
+
+def time_launches(fn, steps: int, warmup: int):
+    """Average per-launch time (s) of `fn` (one kernel launch) over `steps` launches.
+
+    The `steps` launches are captured once into a HIP graph on a side stream and
+    the graph is replayed between two events recorded on that same stream, so the
+    figure is device time without Python dispatch gaps. Falls back to eager
+    launches on the current stream if capture is refused.
+    """
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    try:
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(graph, stream=stream):
+                for _ in range(steps):
+                    fn()
+        torch.cuda.synchronize()
+        graph.replay()  # warm replay
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        graph.replay()
+        end.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / 1e3 / steps
+    except Exception as exc:  # pragma: no cover - capture refused
+        print(f"bench: graph capture failed ({exc!r}); timing eager launches", file=sys.stderr)
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1e3 / steps
+
+
+def load_traffic(name: str):
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
+    calibrated on a copy kernel), committed as profiles/hbm_traffic.json."""
+    p = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        return json.load(f).get(name, {}).get("bytes_per_launch")
+
+
+def bench_qkv(steps, warmup):
+    import torch
+    import joyomni_ops as jo
+    from joyomni_ops.rope import rope_3d_half_tables
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(0)
+    qkv = torch.randn(L_TOK, 3 * E, generator=g).to(torch.bfloat16).to(dev)
+    qw = (1 + 0.1 * torch.randn(HEAD_DIM, generator=g)).to(torch.bfloat16).to(dev)
+    kw = (1 + 0.1 * torch.randn(HEAD_DIM, generator=g)).to(torch.bfloat16).to(dev)
+    cos, sin = rope_3d_half_tables(3, 45, 80, (44, 42, 42), 10000.0, device=dev)
+    q_out = torch.empty(L_TOK, HEADS, HEAD_DIM, dtype=torch.bfloat16, device=dev)
+    k_out = torch.empty_like(q_out)
+    ck = torch.empty(RING_SLOTS, L_TOK, HEADS, HEAD_DIM, dtype=torch.bfloat16, device=dev)
+    cv = torch.empty_like(ck)
+
+    def step():
+        jo.fused_qkv_norm_rope_cache(qkv, HEADS, 1e-6, qw, kw, cos, sin, q_out, k_out, ck, cv, SLOT, 0)
+
+    t = time_launches(step, steps, warmup)
+    return t, qkv_bytes(L_TOK)
+
+
+def bench_gemm(steps, warmup):
+    import torch
+    import joyomni_ops as jo
+    dev = torch.device("cuda:0")
+    res = []
+    for name, K, N in GEMM_SHAPES:
+        g = torch.Generator().manual_seed(K + N)
+        M = L_TOK
+        x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
+        w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+        bias = (torch.randn(N, generator=g) * 0.01).to(torch.bfloat16).to(dev)
+        qa = torch.empty(M, K, dtype=torch.float8_e4m3fn, device=dev)
+        sa = torch.empty(M, 1, device=dev)
+        qw = torch.empty(N, K, dtype=torch.float8_e4m3fn, device=dev)
+        sw = torch.empty(N, 1, device=dev)
+        jo.per_token_quant_fp8(x, qa, sa, True)
+        jo.per_token_quant_fp8(w, qw, sw, True)
+        swr = sw.reshape(1, N)
+        wt = qw.t()
+        fn = jo.fp8_scaled_mm_gelu_tanh if name == "ffn_up" else jo.fp8_scaled_mm
+        t = time_launches(lambda: fn(qa, wt, sa, swr, torch.bfloat16, bias), steps, warmup)
+        flops = 2 * M * N * K
+        res.append({"shape": name, "M": M, "K": K, "N": N, "ms": t * 1e3,
+                    "tflops": flops / t / 1e12, "frac_fp8_peak": flops / t / 1e12 / PEAK_FP8_TFLOPS,
+                    "epilogue": "bias+gelu_tanh" if name == "ffn_up" else "bias"})
+        del x, w, qa, qw
+    tot_flops = sum(2 * r["M"] * r["N"] * r["K"] for r in res)
+    tot_t = sum(r["ms"] for r in res) / 1e3
+    return res, tot_flops / tot_t / 1e12
+
+
+def bench_small_m(steps, warmup):
+    import torch
+    import joyomni_ops as jo
+    dev = torch.device("cuda:0")
+    out = []
+    for N in (15360, 5120):
+        K = 5120
+        g = torch.Generator().manual_seed(N)
+        w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+        qw = torch.empty(N, K, dtype=torch.float8_e4m3fn, device=dev)
+        sw = torch.empty(N, 1, device=dev)
+        jo.per_token_quant_fp8(w, qw, sw, True)
+        bias = torch.zeros(N, dtype=torch.bfloat16, device=dev)
+        for M in SMALL_M:
+            x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
+            qa = torch.empty(M, K, dtype=torch.float8_e4m3fn, device=dev)
+            sa = torch.empty(M, 1, device=dev)
+            jo.per_token_quant_fp8(x, qa, sa, True)
+            t = time_launches(lambda: jo.fp8_scaled_mm(qa, qw.t(), sa, sw.reshape(1, N), torch.bfloat16, bias),
+                              steps, warmup)
+            b = gemm_bytes(M, N, K)
+            out.append({"M": M, "K": K, "N": N, "us": t * 1e6, "gbs": b / t / 1e9,
+                        "frac_hbm_peak": b / t / 1e9 / PEAK_HBM_GBS})
+    return out
+
+
+def bench_quant(steps, warmup):
+    import torch
+    import joyomni_ops as jo
+    dev = torch.device("cuda:0")
+    out = []
+    for K in (5120, 13824):
+        M = L_TOK
+        x = torch.randn(M, K, generator=torch.Generator().manual_seed(K)).to(torch.bfloat16).to(dev)
+        q = torch.empty(M, K, dtype=torch.float8_e4m3fn, device=dev)
+        s = torch.empty(M, 1, device=dev)
+        t = time_launches(lambda: jo.per_token_quant_fp8(x, q, s, True), steps, warmup)
+        b = quant_bytes(M, K)
+        out.append({"M": M, "K": K, "us": t * 1e6, "gbs": b / t / 1e9, "frac_hbm_peak": b / t / 1e9 / PEAK_HBM_GBS})
+    return out
+
+
+def cpu_baseline_qkv():
+    """Reference CPU torch path (oracle/torch_path.py) on a bounded token sample."""
+    import torch
+    from oracle import torch_path
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    Ls = L_TOK  # the whole chunk
+    g = torch.Generator().manual_seed(0)
+    qkv = torch.randn(Ls, 3 * E, generator=g).to(torch.bfloat16)
+    qw = (1 + 0.1 * torch.randn(HEAD_DIM, generator=g)).to(torch.bfloat16)
+    kw = (1 + 0.1 * torch.randn(HEAD_DIM, generator=g)).to(torch.bfloat16)
+    ang = torch.rand(Ls, HEAD_DIM // 2, generator=g)
+    cos, sin = ang.cos().to(torch.bfloat16), ang.sin().to(torch.bfloat16)
+    ck = torch.empty(RING_SLOTS, Ls, HEADS, HEAD_DIM, dtype=torch.bfloat16)
+    cv = torch.empty_like(ck)
+    torch_path.qkv_norm_rope_cache(qkv, HEADS, 1e-6, qw, kw, cos, sin, ck, cv, SLOT)  # warm-up
+    times = []
+    t_end = time.perf_counter() + 20.0
+    while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 15):
+        t0 = time.perf_counter()
+        torch_path.qkv_norm_rope_cache(qkv, HEADS, 1e-6, qw, kw, cos, sin, ck, cv, SLOT)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    t = times[len(times) // 2]
+    return {"value": qkv_bytes(Ls) / t / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"full chunk {Ls} tokens x 40 heads x 128, median of {len(times)} runs, "
+                      f"torch CPU restatement of sgl_fused_ops.py:170-199 + cache copy"}
+
+
+def cpu_baseline_gemm():
+    import torch
+    from oracle import torch_path
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    Ms, K, N = 256, 5120, 15360
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(Ms, K, generator=g).to(torch.bfloat16)
+    wq, ws = torch_path.quantize_per_token((torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16))
+    bias = torch.zeros(N, dtype=torch.bfloat16)
+    torch_path.fp8_linear(x, wq, ws, bias)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        torch_path.fp8_linear(x, wq, ws, bias)
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[1]
+    return {"value": 2 * Ms * N * K / t / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"QKV shape, {Ms} of {L_TOK} rows, median of 3, quant + fp32 dequant-matmul"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default="all", choices=["all", "qkv", "gemm", "small", "quant"])
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
+              "the hot path has no multi-GPU component in this tier.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import joyomni_ops  # noqa: F401  (fails loudly if the HIP library is missing)
+    props = torch.cuda.get_device_properties(0)
+    rec = {"metric": METRIC, "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+           "data": "synthetic (seeded N(0,1) qkv, N(1,0.1) norm weights, real 3-D RoPE tables)",
+           "config": {"workload": "cfg1: fused QKV split + q/k RMSNorm + 3-D RoPE (44/42/42, theta 1e4) "
+                                  "+ KV-ring write (4 slots), outputs q_rope, k_rope, k_pre->cache, v->cache",
+                      "seq_len": L_TOK, "heads": HEADS, "head_dim": HEAD_DIM, "grid_thw": [3, 45, 80],
+                      "parallelism": "single GPU"},
+           "device": {"name": props.name, "arch": getattr(props, "gcnArchName", "?"),
+                      "cus": props.multi_processor_count}}
+    if args.only in ("all", "qkv"):
+        t, b = bench_qkv(args.steps, args.warmup)
+        gbs = b / t / 1e9
+        rec.update({"value": round(gbs, 1), "ms_per_step": t * 1e3})
+        rec["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                           "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": load_traffic("qkv_norm_rope"),
+                           "algorithmic_bytes": b, "kernel": "qk_norm_rope_kernel<128>"}
+    if args.only in ("all", "gemm"):
+        res, agg = bench_gemm(max(5, args.steps // 5), max(2, args.warmup // 2))
+        best = max(res, key=lambda r: r["tflops"])
+        rec["gemm_cfg2"] = {"shapes": res, "aggregate_tflops": round(agg, 1),
+                            "roofline": {"bound": "mfma", "achieved": round(agg, 1), "peak": PEAK_FP8_TFLOPS,
+                                         "unit": "TFLOP/s", "frac": round(agg / PEAK_FP8_TFLOPS, 4),
+                                         "traffic": load_traffic("fp8_gemm_qkv"),
+                                         "best_shape": best["shape"]}}
+        if "value" not in rec:
+            rec.update({"value": round(agg, 1), "unit": "TFLOP/s", "ms_per_step": sum(r["ms"] for r in res)})
+    if args.only in ("all", "small"):
+        rec["gemm_cfg3_small_m"] = bench_small_m(args.steps, args.warmup)
+    if args.only in ("all", "quant"):
+        rec["act_quant"] = bench_quant(args.steps, args.warmup)
+    if not args.no_cpu:
+        if args.only in ("all", "qkv"):
+            rec["cpu_baseline"] = cpu_baseline_qkv()
+        if args.only in ("all", "gemm"):
+            rec["cpu_baseline_gemm"] = cpu_baseline_gemm()
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,205 @@
+// C ABI of libjoyomni_hip: argument validation (mirroring the reference's
+// TORCH_CHECKs), then one kernel launch on the caller's stream.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "../../include/joyomni_hip.h"
+#include "joy_kernels.hpp"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+joy_status fail(joy_status st, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return st;
+}
+
+joy_status ok() {
+  g_err[0] = '\0';
+  return JOY_OK;
+}
+
+joy_status hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return ok();
+  return fail(JOY_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+int joy_abi_version(void) { return JOY_ABI_VERSION; }
+
+const char* joy_last_error(void) { return g_err; }
+
+joy_status joy_per_token_quant_fp8(const void* input, int input_dtype, void* output_q,
+                                   float* output_s, int64_t M, int64_t K, int rounding,
+                                   void* stream) {
+  if (M < 0 || K < 0) return fail(JOY_ERR_INVALID_ARGUMENT, "input must be [M, K]");
+  if (input_dtype != JOY_DTYPE_BF16 && input_dtype != JOY_DTYPE_FP16)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "input must be bfloat16 or float16");
+  if (rounding != JOY_QUANT_DIVIDE && rounding != JOY_QUANT_RECIPROCAL)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "rounding must be JOY_QUANT_DIVIDE or JOY_QUANT_RECIPROCAL");
+  if (M > 0 && !output_s) return fail(JOY_ERR_INVALID_ARGUMENT, "output_s must contain one scale per row");
+  if (M > 0 && K > 0 && (!input || !output_q))
+    return fail(JOY_ERR_INVALID_ARGUMENT, "input and output_q must be non-null");
+  if (M > 0x7fffffffLL * 4) return fail(JOY_ERR_UNSUPPORTED, "M too large");
+  if (M == 0) return ok();
+  return hip_status(joy::launch_per_token_quant(input, input_dtype == JOY_DTYPE_FP16, output_q,
+                                                output_s, M, K, rounding == JOY_QUANT_DIVIDE,
+                                                (hipStream_t)stream),
+                    "per_token_quant_fp8 launch");
+}
+
+joy_status joy_fp8_scaled_mm(const void* mat_a, const void* mat_b, const float* scales_a,
+                             const float* scales_b, const void* bias, void* out, int out_dtype,
+                             int64_t M, int64_t N, int64_t K, int epilogue, void* stream) {
+  if (M < 0 || N < 0 || K < 0) return fail(JOY_ERR_INVALID_ARGUMENT, "mat_a and mat_b shapes cannot be multiplied");
+  if (K % 16 != 0)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "mat_a must be multiple of 16 bytes for memory alignment");
+  if (out_dtype != JOY_DTYPE_BF16 && out_dtype != JOY_DTYPE_FP16)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "out_dtype must be Half or BFloat16");
+  if (N % 8 != 0)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "out must be multiple of 16 bytes for memory alignment");
+  if (epilogue != JOY_EPILOGUE_NONE && epilogue != JOY_EPILOGUE_GELU_TANH)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "unknown epilogue %d", epilogue);
+  if (M > 0x7fffffffLL || N > 0x7fffffffLL || K > 0x7fffffffLL)
+    return fail(JOY_ERR_UNSUPPORTED, "dimensions above 2^31-1 are not supported");
+  if (M == 0 || N == 0) return ok();
+  if (!out || !scales_a || !scales_b || (K > 0 && (!mat_a || !mat_b)))
+    return fail(JOY_ERR_INVALID_ARGUMENT, "mat_a, mat_b, scales and out must be non-null");
+  if (!aligned(mat_a, 16) || !aligned(mat_b, 16) || !aligned(out, 16) || !aligned(scales_b, 16))
+    return fail(JOY_ERR_UNSUPPORTED, "mat_a, mat_b, out and scales_b must be 16-byte aligned");
+  if (!aligned(scales_a, 4) || (bias && !aligned(bias, 2)))
+    return fail(JOY_ERR_INVALID_ARGUMENT, "scales_a and bias must be naturally aligned");
+  joy::GemmArgs g;
+  g.A = mat_a;
+  g.W = mat_b;
+  g.scales_a = scales_a;
+  g.scales_b = scales_b;
+  g.bias = bias;
+  g.C = out;
+  g.M = (int)M;
+  g.N = (int)N;
+  g.K = (int)K;
+  g.ldc = N;
+  g.out_bf16 = out_dtype == JOY_DTYPE_BF16;
+  g.gelu = epilogue == JOY_EPILOGUE_GELU_TANH;
+  g.force_generic = (K == 0);
+  return hip_status(joy::launch_fp8_gemm(g, (hipStream_t)stream), "fp8_scaled_mm launch");
+}
+
+joy_status joy_fused_qk_norm_rope_3d_paired(void* q, void* k, int64_t batch, int64_t seq_len,
+                                            int64_t num_heads, int64_t head_dim, float eps,
+                                            const void* q_weight, const void* k_weight,
+                                            const void* cos, const void* sin, void* k_pre_rope,
+                                            void* stream) {
+  if (batch < 0 || seq_len < 0 || num_heads < 0)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "q must be 3D [batch, seq_len*num_heads, head_dim]");
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "Unsupported head_dim for fused_qk_norm_rope_3d_paired: %lld",
+                (long long)head_dim);
+  if (num_heads > 0x7fffffffLL) return fail(JOY_ERR_UNSUPPORTED, "num_heads too large");
+  const int64_t units = batch * seq_len * num_heads;
+  if (units == 0) return ok();
+  if (!q || !k || !q_weight || !k_weight || !cos || !sin)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "q, k, weights and cos/sin must be non-null");
+  if (!aligned(q, 16) || !aligned(k, 16) || !aligned(q_weight, 16) || !aligned(k_weight, 16) ||
+      !aligned(cos, 8) || !aligned(sin, 8) || (k_pre_rope && !aligned(k_pre_rope, 16)))
+    return fail(JOY_ERR_UNSUPPORTED, "q, k, k_pre_rope and weights must be 16-byte aligned, cos/sin 8-byte aligned");
+  joy::NormRopeArgs a;
+  a.q_in = (const uint16_t*)q;
+  a.k_in = (const uint16_t*)k;
+  a.v_in = nullptr;
+  a.in_stride = num_heads * head_dim;
+  a.q_out = (uint16_t*)q;
+  a.q_out_stride = a.in_stride;
+  a.k_out = (uint16_t*)k;
+  a.k_out_stride = a.in_stride;
+  a.kpre_out = (uint16_t*)k_pre_rope;
+  a.kpre_stride = a.in_stride;
+  a.v_out = nullptr;
+  a.v_out_stride = 0;
+  a.q_weight = (const uint16_t*)q_weight;
+  a.k_weight = (const uint16_t*)k_weight;
+  a.cos = (const uint16_t*)cos;
+  a.sin = (const uint16_t*)sin;
+  a.n_tokens = batch * seq_len;
+  a.table_len = seq_len;
+  a.num_heads = (int)num_heads;
+  a.eps = eps;
+  return hip_status(joy::launch_qk_norm_rope(a, (int)head_dim, (hipStream_t)stream),
+                    "fused_qk_norm_rope_3d_paired launch");
+}
+
+joy_status joy_fused_qkv_norm_rope_cache(const void* qkv, int64_t qkv_row_stride, int64_t seq_len,
+                                         int64_t num_heads, int64_t head_dim, float eps,
+                                         const void* q_weight, const void* k_weight,
+                                         const void* cos, const void* sin, void* q_out,
+                                         int64_t q_out_stride, void* k_out, int64_t k_out_stride,
+                                         void* cache_k, void* cache_v, int64_t num_slots,
+                                         int64_t slot_capacity, int64_t slot, int64_t slot_offset,
+                                         void* stream) {
+  if (seq_len < 0 || num_heads < 0) return fail(JOY_ERR_INVALID_ARGUMENT, "seq_len and num_heads must be >= 0");
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "Unsupported head_dim: %lld", (long long)head_dim);
+  if (num_heads > 0x7fffffffLL) return fail(JOY_ERR_UNSUPPORTED, "num_heads too large");
+  const int64_t E = num_heads * head_dim;
+  if (qkv_row_stride < 3 * E) return fail(JOY_ERR_INVALID_ARGUMENT, "qkv row stride must be >= 3*num_heads*head_dim");
+  if (q_out_stride < E || (k_out && k_out_stride < E))
+    return fail(JOY_ERR_INVALID_ARGUMENT, "q_out/k_out token stride must be >= num_heads*head_dim");
+  if ((cache_k == nullptr) != (cache_v == nullptr))
+    return fail(JOY_ERR_INVALID_ARGUMENT, "cache_k and cache_v must be provided together");
+  if (cache_k) {
+    if (num_slots <= 0 || slot_capacity < 0)
+      return fail(JOY_ERR_INVALID_ARGUMENT, "cache must have num_slots > 0 and slot_capacity >= 0");
+    if (slot < 0 || slot >= num_slots)
+      return fail(JOY_ERR_INVALID_ARGUMENT, "slot %lld out of range [0, %lld)", (long long)slot,
+                  (long long)num_slots);
+    if (slot_offset < 0 || slot_offset + seq_len > slot_capacity)
+      return fail(JOY_ERR_INVALID_ARGUMENT, "tokens [%lld, %lld) do not fit a slot of %lld tokens",
+                  (long long)slot_offset, (long long)(slot_offset + seq_len), (long long)slot_capacity);
+  }
+  if (seq_len == 0 || num_heads == 0) return ok();
+  if (!qkv || !q_out || !q_weight || !k_weight || !cos || !sin)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "qkv, q_out, weights and cos/sin must be non-null");
+  if ((qkv_row_stride % 8) || (q_out_stride % 8) || (k_out && (k_out_stride % 8)))
+    return fail(JOY_ERR_UNSUPPORTED, "token strides must be multiples of 8 elements");
+  if (!aligned(qkv, 16) || !aligned(q_out, 16) || (k_out && !aligned(k_out, 16)) ||
+      (cache_k && (!aligned(cache_k, 16) || !aligned(cache_v, 16))) || !aligned(q_weight, 16) ||
+      !aligned(k_weight, 16) || !aligned(cos, 8) || !aligned(sin, 8))
+    return fail(JOY_ERR_UNSUPPORTED, "tensors must be 16-byte aligned (cos/sin 8-byte)");
+  const uint16_t* base = (const uint16_t*)qkv;
+  joy::NormRopeArgs a;
+  a.q_in = base;
+  a.k_in = base + E;
+  a.v_in = cache_v ? base + 2 * E : nullptr;
+  a.in_stride = qkv_row_stride;
+  a.q_out = (uint16_t*)q_out;
+  a.q_out_stride = q_out_stride;
+  a.k_out = (uint16_t*)k_out;
+  a.k_out_stride = k_out_stride;
+  const int64_t slot_base = cache_k ? (slot * slot_capacity + slot_offset) * E : 0;
+  a.kpre_out = cache_k ? (uint16_t*)cache_k + slot_base : nullptr;
+  a.kpre_stride = E;
+  a.v_out = cache_v ? (uint16_t*)cache_v + slot_base : nullptr;
+  a.v_out_stride = E;
+  a.q_weight = (const uint16_t*)q_weight;
+  a.k_weight = (const uint16_t*)k_weight;
+  a.cos = (const uint16_t*)cos;
+  a.sin = (const uint16_t*)sin;
+  a.n_tokens = seq_len;
+  a.table_len = seq_len;
+  a.num_heads = (int)num_heads;
+  a.eps = eps;
+  return hip_status(joy::launch_qk_norm_rope(a, (int)head_dim, (hipStream_t)stream),
+                    "fused_qkv_norm_rope_cache launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,52 @@
+// Internal launch interface between the C ABI (capi.hip) and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace joy {
+
+// Token-strided [tokens, H, D] bf16 views (strides in elements per token).
+struct NormRopeArgs {
+  const uint16_t* q_in;
+  const uint16_t* k_in;
+  const uint16_t* v_in;  // may be null
+  int64_t in_stride;
+  uint16_t* q_out;
+  int64_t q_out_stride;
+  uint16_t* k_out;  // may be null
+  int64_t k_out_stride;
+  uint16_t* kpre_out;  // may be null
+  int64_t kpre_stride;
+  uint16_t* v_out;  // may be null (requires v_in)
+  int64_t v_out_stride;
+  const uint16_t* q_weight;
+  const uint16_t* k_weight;
+  const uint16_t* cos;  // [table_len, D/2]
+  const uint16_t* sin;
+  int64_t n_tokens;   // tokens processed (B * L)
+  int64_t table_len;  // cos/sin row = token % table_len
+  int num_heads;
+  float eps;
+};
+
+struct GemmArgs {
+  const void* A;  // e4m3fn [M, K] row-major
+  const void* W;  // e4m3fn [N, K] row-major (== (K, N) column-major)
+  const float* scales_a;
+  const float* scales_b;
+  const void* bias;  // out dtype [N] or null
+  void* C;           // [M, N] with row stride ldc
+  int M, N, K;
+  int64_t ldc;
+  bool out_bf16;
+  bool gelu;
+  bool force_generic;
+};
+
+hipError_t launch_per_token_quant(const void* in, bool in_fp16, void* q, float* s, int64_t M,
+                                  int64_t K, bool divide, hipStream_t st);
+hipError_t launch_qk_norm_rope(const NormRopeArgs& a, int head_dim, hipStream_t st);
+hipError_t launch_fp8_gemm(const GemmArgs& g, hipStream_t st);
+
+}  // namespace joy

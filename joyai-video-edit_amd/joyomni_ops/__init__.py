@@ -1,0 +1,476 @@
+"""joyomni_ops -- MI355X (gfx950) drop-in for the reference's operator package.
+
+Same namespace, op schemas, FakeTensor registrations and Python wrappers as the
+reference's ``joyomni_ops/joyomni_ops/__init__.py`` (schemas from
+``joyomni_ops/csrc/pybind.cpp:52-75``), so ``torch.ops.joyomni_ops.*`` and
+``from joyomni_ops import ...`` keep working for ``deploy/xvideo``.
+
+The quantised hot path -- ``sgl_per_token_quant_fp8``, ``fp8_scaled_mm``,
+``fused_qk_norm_rope_3d_paired`` and the new ``fused_qkv_norm_rope_cache`` --
+runs in hand-written gfx950 kernels of ``libjoyomni_hip.so`` reached through
+its C ABI (``include/joyomni_hip.h``). Importing fails when that library is
+missing, exactly like the reference (``__init__.py:15-19``); nothing falls back.
+
+Ops outside the quantised path (``fused_joint_qkv_pack``,
+``fused_cached_kv_pack``, ``fused_norm_scale_shift``, ``rmsnorm``) keep their
+reference schemas and are composed from torch device ops, so the reference's
+imports (``sgl_fused_ops.py:27-33``) still resolve.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+_LIB = _lib.load()  # raises ImportError when the HIP library is not built
+
+__all__ = [
+    "fused_qk_norm_rope_3d_paired",
+    "fused_joint_qkv_pack",
+    "fused_cached_kv_pack",
+    "fused_norm_scale_shift",
+    "rmsnorm",
+    "sgl_per_token_quant_fp8",
+    "fp8_scaled_mm",
+    "has_quant",
+    "has_fp8",
+    # additions of this build
+    "per_token_quant_fp8",
+    "fp8_scaled_mm_gelu_tanh",
+    "fused_qkv_norm_rope_cache",
+]
+
+_NS = "joyomni_ops"
+_lib_def = torch.library.Library(_NS, "DEF")
+
+# --- reference schemas (pybind.cpp:52-75), unchanged ---
+_lib_def.define(
+    "fused_qk_norm_rope_3d_paired(Tensor! q, Tensor! k, int seq_len, int num_heads, float eps, "
+    "Tensor q_weight, Tensor k_weight, Tensor cos, Tensor sin, Tensor? k_pre_rope) -> ()")
+_lib_def.define(
+    "fused_joint_qkv_pack(Tensor img_q, Tensor img_k, Tensor img_v, "
+    "Tensor txt_q, Tensor txt_k, Tensor txt_v, Tensor? cached_k, Tensor? cached_v, "
+    "Tensor txt_q_weight, Tensor txt_k_weight, float eps) -> (Tensor, Tensor, Tensor)")
+_lib_def.define(
+    "fused_cached_kv_pack(Tensor key0, Tensor value0, Tensor? key1, Tensor? value1, "
+    "Tensor cos, Tensor sin) -> (Tensor, Tensor)")
+_lib_def.define(
+    "fused_norm_scale_shift(Tensor x, Tensor? gamma_opt, Tensor? beta_opt, "
+    "Tensor scale, Tensor shift, int norm_type, float eps) -> Tensor")
+_lib_def.define("rmsnorm(Tensor x, Tensor weight, float eps) -> Tensor")
+_lib_def.define("sgl_per_token_quant_fp8(Tensor input, Tensor! output_q, Tensor! output_s) -> ()")
+_lib_def.define(
+    "fp8_scaled_mm(Tensor mat_a, Tensor mat_b, Tensor scales_a, Tensor scales_b, "
+    "ScalarType out_dtype, Tensor? bias) -> Tensor")
+
+# --- additions of this build ---
+_lib_def.define(
+    "per_token_quant_fp8(Tensor input, Tensor! output_q, Tensor! output_s, bool exact_division) -> ()")
+_lib_def.define(
+    "fp8_scaled_mm_gelu_tanh(Tensor mat_a, Tensor mat_b, Tensor scales_a, Tensor scales_b, "
+    "ScalarType out_dtype, Tensor? bias) -> Tensor")
+_lib_def.define(
+    "fused_qkv_norm_rope_cache(Tensor qkv, int num_heads, float eps, Tensor q_weight, "
+    "Tensor k_weight, Tensor cos, Tensor sin, Tensor(a!) q_out, Tensor(b!)? k_out, "
+    "Tensor(c!)? cache_k, Tensor(d!)? cache_v, int slot, int slot_offset) -> ()")
+
+_ops = torch.ops.joyomni_ops
+
+
+# --------------------------------------------------------------------------
+# argument checks, worded like the reference's TORCH_CHECKs (joyomni_ops.h:8-15)
+# --------------------------------------------------------------------------
+def _check(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _check_input(t: torch.Tensor, name: str, dtype: torch.dtype) -> None:
+    _check(t.is_cuda, f"{name} must be a CUDA tensor")
+    _check(t.is_contiguous(), f"{name} must be contiguous")
+    _check(t.dtype == dtype, f"{name} dtype is {t.dtype}, expected {dtype}")
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+_OUT_CODE = {torch.bfloat16: _lib.JOY_DTYPE_BF16, torch.float16: _lib.JOY_DTYPE_FP16}
+
+
+# --------------------------------------------------------------------------
+# quantiser
+# --------------------------------------------------------------------------
+def _quant_impl(input, output_q, output_s, rounding):
+    for name, t in (("input", input), ("output_q", output_q), ("output_s", output_s)):
+        _check(t.is_cuda, f"{name} must be a CUDA tensor")
+        _check(t.is_contiguous(), f"{name} must be contiguous")
+    _check(input.dim() == 2, "input must be [M, K]")
+    _check(output_q.shape == input.shape, "output_q shape must match input")
+    _check(output_q.dtype == torch.float8_e4m3fn, "output_q must be torch.float8_e4m3fn")
+    _check(output_s.dtype == torch.float32, "output_s must be float32")
+    _check(output_s.numel() == input.size(0), "output_s must contain one scale per row")
+    _check(input.device == output_q.device and input.device == output_s.device,
+           "input and outputs must be on the same device")
+    _check(input.dtype in (torch.bfloat16, torch.float16), "input must be bfloat16 or float16")
+    M, K = input.shape
+    with torch.cuda.device(input.device):
+        st = _LIB.joy_per_token_quant_fp8(
+            _ptr(input), _OUT_CODE[input.dtype], _ptr(output_q), _ptr(output_s), M, K, rounding,
+            _stream(input))
+    _lib.check(_LIB, st)
+
+
+@torch.library.impl(_lib_def, "sgl_per_token_quant_fp8", "CUDA")
+def _sgl_per_token_quant_fp8_cuda(input, output_q, output_s):
+    # The reference's gfx950 kernel rounds by reciprocal multiply
+    # (per_token_quant_fp8_rocm.hip:72-77); keep that contract for this op.
+    _quant_impl(input, output_q, output_s, _lib.JOY_QUANT_RECIPROCAL)
+
+
+@torch.library.impl(_lib_def, "per_token_quant_fp8", "CUDA")
+def _per_token_quant_fp8_cuda(input, output_q, output_s, exact_division):
+    _quant_impl(input, output_q, output_s,
+                _lib.JOY_QUANT_DIVIDE if exact_division else _lib.JOY_QUANT_RECIPROCAL)
+
+
+# --------------------------------------------------------------------------
+# GEMM
+# --------------------------------------------------------------------------
+def _scaled_mm_impl(mat_a, mat_b, scales_a, scales_b, out_dtype, bias, epilogue):
+    # checks of fp8_gemm.cu:1457-1487
+    _check(mat_a.is_cuda, "mat_a must be a CUDA tensor")
+    _check(mat_b.is_cuda, "mat_b must be a CUDA tensor")
+    _check(mat_a.dim() == 2, "mat_a must be a 2D tensor")
+    _check(mat_b.dim() == 2, "mat_b must be a 2D tensor")
+    _check(mat_a.stride(1) == 1, "mat_a must be a row major tensor")
+    _check(mat_b.stride(0) == 1, "mat_b must be a column major tensor")
+    _check(mat_a.size(1) == mat_b.size(0), "mat_a and mat_b shapes cannot be multiplied")
+    _check((mat_a.size(1) * mat_a.element_size()) % 16 == 0,
+           "mat_a must be multiple of 16 bytes for memory alignment")
+    _check((mat_b.size(0) * mat_b.element_size()) % 16 == 0,
+           "mat_b must be multiple of 16 bytes for memory alignment")
+    _check(mat_a.dtype == torch.float8_e4m3fn, "mat_a must be Float8_e4m3fn")
+    _check(mat_b.dtype == torch.float8_e4m3fn, "mat_b must be Float8_e4m3fn")
+    _check(out_dtype in (torch.float16, torch.bfloat16), "out_dtype must be Half or BFloat16")
+    _check(scales_a.numel() == mat_a.size(0), "size of scales_a is not matched")
+    _check(scales_b.numel() == mat_b.size(1), "size of scales_b is not matched")
+    _check(scales_a.is_contiguous(), "scales_a must be contiguous")
+    _check(scales_b.is_contiguous(), "scales_b msut be contiguous")
+    _check(scales_a.dtype == torch.float32, "scales_a must be Float32")
+    _check(scales_b.dtype == torch.float32, "scales_b must be Float32")
+    if bias is not None:
+        _check(bias.numel() == mat_b.size(1), "size of bias is not matched")
+        _check(bias.is_contiguous(), "bias must be contiguous")
+        _check(bias.dtype == out_dtype, "bias dtype must match output dtype")
+    M, K = mat_a.shape
+    N = mat_b.size(1)
+    # Row stride of A and column stride of B must be K (dense rows).
+    _check(M <= 1 or mat_a.stride(0) == K, "mat_a rows must be dense (stride(0) == K)")
+    _check(N <= 1 or mat_b.stride(1) == K, "mat_b columns must be dense (stride(1) == K)")
+    out = torch.empty((M, N), device=mat_a.device, dtype=out_dtype)
+    _check((out.size(1) * out.element_size()) % 16 == 0,
+           "out must be multiple of 16 bytes for memory alignment")
+    with torch.cuda.device(mat_a.device):
+        st = _LIB.joy_fp8_scaled_mm(
+            _ptr(mat_a), _ptr(mat_b), _ptr(scales_a), _ptr(scales_b), _ptr(bias), _ptr(out),
+            _OUT_CODE[out_dtype], M, N, K, epilogue, _stream(mat_a))
+    _lib.check(_LIB, st)
+    return out
+
+
+@torch.library.impl(_lib_def, "fp8_scaled_mm", "CUDA")
+def _fp8_scaled_mm_cuda(mat_a, mat_b, scales_a, scales_b, out_dtype, bias=None):
+    return _scaled_mm_impl(mat_a, mat_b, scales_a, scales_b, out_dtype, bias, _lib.JOY_EPILOGUE_NONE)
+
+
+@torch.library.impl(_lib_def, "fp8_scaled_mm_gelu_tanh", "CUDA")
+def _fp8_scaled_mm_gelu_cuda(mat_a, mat_b, scales_a, scales_b, out_dtype, bias=None):
+    return _scaled_mm_impl(mat_a, mat_b, scales_a, scales_b, out_dtype, bias,
+                           _lib.JOY_EPILOGUE_GELU_TANH)
+
+
+# --------------------------------------------------------------------------
+# q/k RMSNorm + RoPE
+# --------------------------------------------------------------------------
+@torch.library.impl(_lib_def, "fused_qk_norm_rope_3d_paired", "CUDA")
+def _fused_qk_norm_rope_3d_paired_cuda(q, k, seq_len, num_heads, eps, q_weight, k_weight, cos,
+                                       sin, k_pre_rope=None):
+    # checks of fused_qknorm_rope_3d_kernel.cu:285-310
+    _check(q.dim() == 3, "q must be 3D [batch, seq_len*num_heads, head_dim]")
+    _check(k.dim() == 3, "k must be 3D [batch, seq_len*num_heads, head_dim]")
+    _check(q.shape == k.shape, "q and k must have the same shape")
+    _check(q_weight.dim() == 1 and k_weight.dim() == 1, "weights must be 1D [head_dim]")
+    _check(cos.dim() == 2 and sin.dim() == 2, "cos/sin must be 2D [seq_len, head_dim/2]")
+    for name, t in (("q", q), ("k", k), ("q_weight", q_weight), ("k_weight", k_weight),
+                    ("cos", cos), ("sin", sin)):
+        _check_input(t, name, torch.bfloat16)
+    batch, _, head_dim = q.shape
+    _check(q.size(1) == seq_len * num_heads, "q.size(1) must equal seq_len*num_heads")
+    _check(q_weight.size(0) == head_dim and k_weight.size(0) == head_dim,
+           "weight size must match head_dim")
+    _check(cos.size(0) == seq_len and cos.size(1) == head_dim // 2,
+           "cos shape must be [seq_len, head_dim/2]")
+    _check(sin.size(0) == seq_len and sin.size(1) == head_dim // 2,
+           "sin shape must be [seq_len, head_dim/2]")
+    if k_pre_rope is not None:
+        _check(k_pre_rope.shape == k.shape, "k_pre_rope must have the same shape as k")
+        _check_input(k_pre_rope, "k_pre_rope", torch.bfloat16)
+    with torch.cuda.device(q.device):
+        st = _LIB.joy_fused_qk_norm_rope_3d_paired(
+            _ptr(q), _ptr(k), batch, seq_len, num_heads, head_dim, float(eps), _ptr(q_weight),
+            _ptr(k_weight), _ptr(cos), _ptr(sin), _ptr(k_pre_rope), _stream(q))
+    _lib.check(_LIB, st)
+
+
+def _token_stride(t: torch.Tensor, H: int, D: int, name: str) -> int:
+    """Token stride of a [L, H, D] (or [1, L, H, D] / [L, H*D]) view with dense heads."""
+    x = t
+    if x.dim() == 4:
+        _check(x.size(0) == 1, f"{name} batch must be 1")
+        x = x[0]
+    if x.dim() == 2:
+        _check(x.size(1) == H * D and x.stride(1) == 1, f"{name} must have dense rows of H*D")
+        return x.stride(0)
+    _check(x.dim() == 3 and x.size(1) == H and x.size(2) == D, f"{name} must be [L, H, D]")
+    _check(x.stride(2) == 1 and x.stride(1) == D, f"{name} must have dense heads")
+    return x.stride(0)
+
+
+@torch.library.impl(_lib_def, "fused_qkv_norm_rope_cache", "CUDA")
+def _fused_qkv_norm_rope_cache_cuda(qkv, num_heads, eps, q_weight, k_weight, cos, sin, q_out,
+                                    k_out, cache_k, cache_v, slot, slot_offset):
+    _check(qkv.is_cuda, "qkv must be a CUDA tensor")
+    _check(qkv.dtype == torch.bfloat16, f"qkv dtype is {qkv.dtype}, expected torch.bfloat16")
+    x = qkv[0] if qkv.dim() == 3 else qkv
+    _check(qkv.dim() in (2, 3) and (qkv.dim() == 2 or qkv.size(0) == 1),
+           "qkv must be [L, 3*H*D] or [1, L, 3*H*D]")
+    _check(x.stride(-1) == 1, "qkv rows must be contiguous")
+    L, E3 = x.shape
+    H = int(num_heads)
+    _check(H > 0 and E3 % (3 * H) == 0, "qkv width must be 3*num_heads*head_dim")
+    D = E3 // (3 * H)
+    for name, t in (("q_weight", q_weight), ("k_weight", k_weight), ("cos", cos), ("sin", sin)):
+        _check_input(t, name, torch.bfloat16)
+    _check(q_weight.numel() == D and k_weight.numel() == D, "weight size must match head_dim")
+    _check(cos.shape == (L, D // 2) and sin.shape == (L, D // 2),
+           "cos/sin shape must be [seq_len, head_dim/2]")
+    q_stride = _token_stride(q_out, H, D, "q_out")
+    k_stride = _token_stride(k_out, H, D, "k_out") if k_out is not None else 0
+    for name, t in (("q_out", q_out), ("k_out", k_out), ("cache_k", cache_k), ("cache_v", cache_v)):
+        if t is not None:
+            _check(t.is_cuda and t.dtype == torch.bfloat16, f"{name} must be a bf16 CUDA tensor")
+    n_slots = cap = 0
+    if (cache_k is None) != (cache_v is None):
+        raise RuntimeError("cache_k and cache_v must be provided together")
+    if cache_k is not None:
+        _check(cache_k.is_contiguous() and cache_v.is_contiguous(), "cache_k/cache_v must be contiguous")
+        _check(cache_k.dim() == 4 and cache_k.shape == cache_v.shape
+               and cache_k.shape[2:] == (H, D), "cache must be [num_slots, capacity, H, D]")
+        n_slots, cap = cache_k.shape[0], cache_k.shape[1]
+    with torch.cuda.device(qkv.device):
+        st = _LIB.joy_fused_qkv_norm_rope_cache(
+            _ptr(x), x.stride(0), L, H, D, float(eps), _ptr(q_weight), _ptr(k_weight), _ptr(cos),
+            _ptr(sin), _ptr(q_out), q_stride, _ptr(k_out), k_stride, _ptr(cache_k), _ptr(cache_v),
+            n_slots, cap, int(slot), int(slot_offset), _stream(qkv))
+    _lib.check(_LIB, st)
+
+
+# --------------------------------------------------------------------------
+# ops outside the quantised path: torch device compositions of the reference
+# semantics (sgl_fused_ops.py:202-209,257-265; fused_joint_qkv_pack.cu:58-79,210-219;
+# fused_norm_scale_shift.cu; rmsnorm.cu)
+# --------------------------------------------------------------------------
+def _rms_two_round(x, w, eps):
+    xf = x.float()
+    n = (xf * torch.rsqrt(xf.square().mean(-1, keepdim=True) + eps)).to(torch.bfloat16)
+    return n * w.to(torch.bfloat16)
+
+
+@torch.library.impl(_lib_def, "fused_joint_qkv_pack", "CUDA")
+def _fused_joint_qkv_pack_cuda(img_q, img_k, img_v, txt_q, txt_k, txt_v, cached_k, cached_v,
+                               txt_q_weight, txt_k_weight, eps):
+    if (cached_k is None) != (cached_v is None):
+        raise RuntimeError("cached_k and cached_v must be provided together")
+    q = torch.cat((img_q, _rms_two_round(txt_q, txt_q_weight, eps)), dim=1)
+    k = torch.cat((img_k, _rms_two_round(txt_k, txt_k_weight, eps)), dim=1)
+    v = torch.cat((img_v, txt_v), dim=1)
+    if cached_k is not None:
+        k = torch.cat((cached_k, k), dim=1)
+        v = torch.cat((cached_v, v), dim=1)
+    return q.contiguous(), k.contiguous(), v.contiguous()
+
+
+@torch.library.impl(_lib_def, "fused_cached_kv_pack", "CUDA")
+def _fused_cached_kv_pack_cuda(key0, value0, key1, value1, cos, sin):
+    keys = [key0] + ([key1] if key1 is not None else [])
+    vals = [value0] + ([value1] if value1 is not None else [])
+    k = torch.cat(keys, dim=1).float()
+    B, L, H, D = k.shape
+    pairs = k.reshape(B, L, H, D // 2, 2)
+    rot = torch.stack((-pairs[..., 1], pairs[..., 0]), dim=-1).flatten(-2)
+    c = cos.reshape(1, L, 1, D).float()
+    s = sin.reshape(1, L, 1, D).float()
+    out_k = (k * c + rot * s).to(key0.dtype)
+    return out_k, torch.cat(vals, dim=1).contiguous()
+
+
+@torch.library.impl(_lib_def, "fused_norm_scale_shift", "CUDA")
+def _fused_norm_scale_shift_cuda(x, gamma_opt, beta_opt, scale, shift, norm_type, eps):
+    xf = x.float()
+    if norm_type == 0:
+        y = torch.nn.functional.layer_norm(xf, (x.shape[-1],), eps=eps)
+    elif norm_type == 1:
+        y = xf * torch.rsqrt(xf.square().mean(-1, keepdim=True) + eps)
+    else:
+        raise RuntimeError("norm_type must be 'layer' or 'rms'")
+    if gamma_opt is not None:
+        y = y * gamma_opt.float()
+    if beta_opt is not None:
+        y = y + beta_opt.float()
+    return (y * (1 + scale.float()) + shift.float()).to(x.dtype)
+
+
+@torch.library.impl(_lib_def, "rmsnorm", "CUDA")
+def _rmsnorm_cuda(x, weight, eps):
+    xf = x.float()
+    return ((xf * torch.rsqrt(xf.square().mean(-1, keepdim=True) + eps)) * weight.float()).to(x.dtype)
+
+
+# --------------------------------------------------------------------------
+# FakeTensor kernels (reference __init__.py:39-101) so torch.compile keeps the
+# ops opaque inside one graph.
+# --------------------------------------------------------------------------
+@torch.library.register_fake("joyomni_ops::fused_qk_norm_rope_3d_paired")
+def _fake_fused_qk_norm_rope_3d_paired(q, k, seq_len, num_heads, eps, q_weight, k_weight, cos,
+                                       sin, k_pre_rope=None):
+    return None
+
+
+@torch.library.register_fake("joyomni_ops::fused_joint_qkv_pack")
+def _fake_fused_joint_qkv_pack(img_q, img_k, img_v, txt_q, txt_k, txt_v, cached_k, cached_v,
+                               txt_q_weight, txt_k_weight, eps):
+    batch, img_len, heads, head_dim = img_q.shape
+    txt_len = txt_q.shape[1]
+    cache_len = cached_k.shape[1] if cached_k is not None else 0
+    out_q = img_q.new_empty((batch, img_len + txt_len, heads, head_dim))
+    out_k = img_q.new_empty((batch, cache_len + img_len + txt_len, heads, head_dim))
+    return out_q, out_k, torch.empty_like(out_k)
+
+
+@torch.library.register_fake("joyomni_ops::fused_cached_kv_pack")
+def _fake_fused_cached_kv_pack(key0, value0, key1, value1, cos, sin):
+    batch, len0, heads, head_dim = key0.shape
+    len1 = key1.shape[1] if key1 is not None else 0
+    out_key = key0.new_empty((batch, len0 + len1, heads, head_dim))
+    return out_key, torch.empty_like(out_key)
+
+
+@torch.library.register_fake("joyomni_ops::fused_norm_scale_shift")
+def _fake_fused_norm_scale_shift(x, gamma, beta, scale, shift, norm_type, eps):
+    return torch.empty_like(x)
+
+
+@torch.library.register_fake("joyomni_ops::rmsnorm")
+def _fake_rmsnorm(x, weight, eps):
+    return torch.empty_like(x)
+
+
+@torch.library.register_fake("joyomni_ops::sgl_per_token_quant_fp8")
+def _fake_sgl_per_token_quant_fp8(input, output_q, output_s):
+    return None
+
+
+@torch.library.register_fake("joyomni_ops::per_token_quant_fp8")
+def _fake_per_token_quant_fp8(input, output_q, output_s, exact_division):
+    return None
+
+
+@torch.library.register_fake("joyomni_ops::fp8_scaled_mm")
+def _fake_fp8_scaled_mm(mat_a, mat_b, scales_a, scales_b, out_dtype, bias=None):
+    return mat_a.new_empty((mat_a.shape[0], mat_b.shape[1]), dtype=out_dtype)
+
+
+@torch.library.register_fake("joyomni_ops::fp8_scaled_mm_gelu_tanh")
+def _fake_fp8_scaled_mm_gelu_tanh(mat_a, mat_b, scales_a, scales_b, out_dtype, bias=None):
+    return mat_a.new_empty((mat_a.shape[0], mat_b.shape[1]), dtype=out_dtype)
+
+
+@torch.library.register_fake("joyomni_ops::fused_qkv_norm_rope_cache")
+def _fake_fused_qkv_norm_rope_cache(qkv, num_heads, eps, q_weight, k_weight, cos, sin, q_out,
+                                    k_out, cache_k, cache_v, slot, slot_offset):
+    return None
+
+
+# --------------------------------------------------------------------------
+# Python wrappers with the reference's names and signatures (__init__.py:104-153)
+# --------------------------------------------------------------------------
+def fused_qk_norm_rope_3d_paired(q, k, seq_len, num_heads, eps, q_weight, k_weight, cos, sin,
+                                 k_pre_rope=None):
+    """In-place fused RMSNorm(q,k) + 3D RoPE. q/k: [B, seq_len*num_heads, head_dim] bf16."""
+    _ops.fused_qk_norm_rope_3d_paired(q, k, seq_len, num_heads, eps, q_weight, k_weight, cos, sin,
+                                      k_pre_rope)
+
+
+def fused_joint_qkv_pack(img_q, img_k, img_v, txt_q, txt_k, txt_v, cached_k, cached_v,
+                         txt_q_weight, txt_k_weight, eps=1e-6):
+    """Pack joint-attention Q/K/V and fuse text Q/K RMSNorm (bf16, B=1, D=128)."""
+    return _ops.fused_joint_qkv_pack(img_q, img_k, img_v, txt_q, txt_k, txt_v, cached_k, cached_v,
+                                     txt_q_weight, txt_k_weight, eps)
+
+
+def fused_cached_kv_pack(key0, value0, key1, value1, cos, sin):
+    """Rotate and pack one or two pre-RoPE cache segments (bf16, B=1, D=128)."""
+    return _ops.fused_cached_kv_pack(key0, value0, key1, value1, cos, sin)
+
+
+def fused_norm_scale_shift(x, gamma, beta, scale, shift, norm_type, eps=1e-5):
+    """Norm(x; gamma, beta) * (1 + scale) + shift. norm_type: 'layer' or 'rms'."""
+    nt = 0 if norm_type == "layer" else 1 if norm_type == "rms" else -1
+    return _ops.fused_norm_scale_shift(x, gamma, beta, scale, shift, nt, eps)
+
+
+def rmsnorm(x, weight, eps=1e-6):
+    """(x / RMS(x)) * weight. x: [M, N], weight: [N]."""
+    return _ops.rmsnorm(x, weight, eps)
+
+
+def has_fp8() -> bool:
+    return hasattr(_ops, "fp8_scaled_mm")
+
+
+def has_quant() -> bool:
+    return hasattr(_ops, "sgl_per_token_quant_fp8")
+
+
+def sgl_per_token_quant_fp8(input, output_q, output_s):
+    _ops.sgl_per_token_quant_fp8(input, output_q, output_s)
+
+
+def fp8_scaled_mm(mat_a, mat_b, scales_a, scales_b, out_dtype, bias: Optional[torch.Tensor] = None):
+    return _ops.fp8_scaled_mm(mat_a, mat_b, scales_a, scales_b, out_dtype, bias)
+
+
+def per_token_quant_fp8(input, output_q, output_s, exact_division: bool = True):
+    """Per-token e4m3fn quantisation; exact_division=True is bit-identical to
+    ``_quantize_per_token_impl`` (deploy/xvideo/models/dit/fp8_linear.py:38-43)."""
+    _ops.per_token_quant_fp8(input, output_q, output_s, exact_division)
+
+
+def fp8_scaled_mm_gelu_tanh(mat_a, mat_b, scales_a, scales_b, out_dtype,
+                            bias: Optional[torch.Tensor] = None):
+    """fp8_scaled_mm followed by GELU-tanh on the rounded output, in one kernel."""
+    return _ops.fp8_scaled_mm_gelu_tanh(mat_a, mat_b, scales_a, scales_b, out_dtype, bias)
+
+
+def fused_qkv_norm_rope_cache(qkv, num_heads, eps, q_weight, k_weight, cos, sin, q_out,
+                              k_out=None, cache_k=None, cache_v=None, slot=0, slot_offset=0):
+    """QKV split + q/k RMSNorm + RoPE in one pass; pre-RoPE K and V land in ring slot `slot`."""
+    _ops.fused_qkv_norm_rope_cache(qkv, num_heads, eps, q_weight, k_weight, cos, sin, q_out, k_out,
+                                   cache_k, cache_v, slot, slot_offset)

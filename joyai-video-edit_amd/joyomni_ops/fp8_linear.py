@@ -1,0 +1,94 @@
+"""FP8 linear layer on the gfx950 kernels -- counterpart of the reference's
+``deploy/xvideo/models/dit/fp8_linear.py``.
+
+Same API (``available``, ``backend``, ``Fp8Linear.from_linear``, ``forward``,
+``_quantize_weight_per_channel``) and the same numerics contract:
+
+* weights: per-output-channel e4m3fn with ``s_w = max(absmax, 1e-8) / 448`` and
+  division (``fp8_linear.py:77-85``), stored as the (K, N) column-major view;
+* activations: per-token e4m3fn with division (``_quantize_per_token_impl``,
+  ``fp8_linear.py:38-43``) for every K -- the reference switches between a
+  reciprocal-multiply HIP kernel (K < 8192) and an Inductor/Triton kernel
+  (K >= 8192) on ROCm (``fp8_linear.py:57-74``); here one kernel, bit-identical to
+  the formula, serves all K;
+* GEMM: ``y = bf16(fma(acc * s_w[n], s_x[m], bias[n]))`` (``fp8_gemm.cu:99-136``)
+  in place of ``torch._scaled_mm`` (``fp8_linear.py:124-132``). An optional
+  fused GELU-tanh epilogue serves the MLP up-projection (``dit.py:87-89,508-513``).
+
+The reference picks torch._scaled_mm whenever ROCm is detected
+(``fp8_linear.py:21,119``); this module always routes to joyomni_ops, which
+reports ``has_fp8() == True``.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+import torch.nn as nn
+
+from . import fp8_scaled_mm, fp8_scaled_mm_gelu_tanh, has_fp8, has_quant, per_token_quant_fp8
+
+FP8_DTYPE = torch.float8_e4m3fn
+FP8_MAX = torch.finfo(FP8_DTYPE).max
+
+
+def available() -> bool:
+    return bool(has_fp8() and has_quant())
+
+
+def backend() -> str:
+    return "joyomni_ops/gfx950-hip" if available() else "unavailable"
+
+
+def quantize_per_token(x_2d: torch.Tensor):
+    """x [M, K] bf16/fp16 (contiguous, on the GPU) -> (q e4m3fn [M, K], s fp32 [M, 1])."""
+    q = torch.empty_like(x_2d, dtype=FP8_DTYPE)
+    s = torch.empty((x_2d.shape[0], 1), device=x_2d.device, dtype=torch.float32)
+    per_token_quant_fp8(x_2d, q, s, True)
+    return q, s
+
+
+def _quantize_weight_per_channel(w_bf16: torch.Tensor):
+    """W [N, K] bf16 -> (Wq as (K, N) with stride (1, K), s_w (1, N) fp32)."""
+    w = w_bf16.to(torch.bfloat16).contiguous()
+    N, K = w.shape
+    wq, s = quantize_per_token(w)
+    w_q_cm = wq.t()
+    assert w_q_cm.shape == (K, N) and w_q_cm.stride() == (1, K)
+    return w_q_cm, s.reshape(1, N).contiguous()
+
+
+class Fp8Linear(nn.Module):
+    def __init__(self, weight_fp8: torch.Tensor, weight_scale: torch.Tensor,
+                 bias: Optional[torch.Tensor], out_dtype: torch.dtype = torch.bfloat16,
+                 gelu_tanh: bool = False):
+        super().__init__()
+        self.register_buffer("weight_fp8", weight_fp8, persistent=False)
+        self.register_buffer("weight_scale", weight_scale, persistent=False)
+        if bias is not None:
+            self.register_buffer("bias", bias.contiguous(), persistent=False)
+        else:
+            self.bias = None
+        self.out_dtype = out_dtype
+        self.gelu_tanh = gelu_tanh
+        K, N = weight_fp8.shape
+        self.in_features = K
+        self.out_features = N
+
+    @classmethod
+    def from_linear(cls, lin: nn.Linear, out_dtype: torch.dtype = torch.bfloat16,
+                    gelu_tanh: bool = False) -> "Fp8Linear":
+        assert available(), "joyomni_ops fp8 ops not available; cannot build Fp8Linear"
+        w_q, w_s = _quantize_weight_per_channel(lin.weight.data.to(torch.bfloat16))
+        b = lin.bias.data.to(dtype=out_dtype) if lin.bias is not None else None
+        return cls(w_q, w_s, b, out_dtype=out_dtype, gelu_tanh=gelu_tanh)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        orig_shape = x.shape
+        x_2d = x.reshape(-1, orig_shape[-1]).contiguous()
+        M, K = x_2d.shape
+        assert K == self.in_features, f"in features mismatch {K} vs {self.in_features}"
+        x_q, x_scale = quantize_per_token(x_2d)
+        mm = fp8_scaled_mm_gelu_tanh if self.gelu_tanh else fp8_scaled_mm
+        y = mm(x_q, self.weight_fp8, x_scale, self.weight_scale, self.out_dtype, self.bias)
+        return y.reshape(*orig_shape[:-1], self.out_features)

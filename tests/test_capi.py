@@ -1,0 +1,87 @@
+"""The C-ABI library loads, exports every symbol include/joyomni_hip.h declares,
+and rejects bad arguments before touching the GPU (no compute calls here)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "joyomni_hip.h")
+
+from joyomni_ops import _lib  # noqa: E402  (conftest puts the package dir on sys.path)
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"JOY_API\s+[\w\s\*]+?\b(joy_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail(f"{_lib.LIB_PATH} missing: run __graft_entry__.build()")
+    return _lib.load()
+
+
+def test_header_declares_expected_entry_points():
+    names = declared_functions()
+    assert names == sorted(_lib.SIGNATURES), names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    for name in declared_functions():
+        assert name in exported, name
+    # nothing else with the joy_ prefix leaks out
+    assert {n for n in exported if n.startswith("joy_")} == set(declared_functions())
+
+
+def test_abi_version(lib):
+    assert lib.joy_abi_version() == _lib.ABI_VERSION
+
+
+def _status(lib, st, code, fragment):
+    assert st == code, lib.joy_last_error()
+    assert fragment in lib.joy_last_error().decode()
+
+
+def test_quant_argument_checks(lib):
+    p = ctypes.c_void_p(0x1000)
+    _status(lib, lib.joy_per_token_quant_fp8(p, 7, p, p, 4, 16, 0, None), 1, "bfloat16 or float16")
+    _status(lib, lib.joy_per_token_quant_fp8(p, 0, p, p, 4, 16, 5, None), 1, "rounding")
+    _status(lib, lib.joy_per_token_quant_fp8(p, 0, p, None, 4, 16, 0, None), 1, "one scale per row")
+    _status(lib, lib.joy_per_token_quant_fp8(p, 0, p, p, -1, 16, 0, None), 1, "[M, K]")
+    assert lib.joy_per_token_quant_fp8(None, 0, None, None, 0, 16, 0, None) == 0  # empty: no launch
+
+
+def test_gemm_argument_checks(lib):
+    p = ctypes.c_void_p(0x1000)
+    args = lambda **kw: [kw.get("a", p), kw.get("b", p), p, p, None, p, kw.get("dt", 0),  # noqa: E731
+                         kw.get("M", 64), kw.get("N", 64), kw.get("K", 64), kw.get("epi", 0), None]
+    _status(lib, lib.joy_fp8_scaled_mm(*args(K=40)), 1, "multiple of 16 bytes")
+    _status(lib, lib.joy_fp8_scaled_mm(*args(N=36)), 1, "out must be multiple of 16 bytes")
+    _status(lib, lib.joy_fp8_scaled_mm(*args(dt=5)), 1, "Half or BFloat16")
+    _status(lib, lib.joy_fp8_scaled_mm(*args(epi=9)), 1, "epilogue")
+    _status(lib, lib.joy_fp8_scaled_mm(*args(a=ctypes.c_void_p(0x1008))), 2, "16-byte aligned")
+    assert lib.joy_fp8_scaled_mm(*args(M=0)) == 0
+
+
+def test_norm_rope_argument_checks(lib):
+    p = ctypes.c_void_p(0x1000)
+    _status(lib, lib.joy_fused_qk_norm_rope_3d_paired(p, p, 1, 4, 2, 96, 1e-6, p, p, p, p, None, None),
+            1, "Unsupported head_dim")
+    _status(lib, lib.joy_fused_qk_norm_rope_3d_paired(p, p, 1, 4, 2, 128, 1e-6, None, p, p, p, None, None),
+            1, "non-null")
+    f = lib.joy_fused_qkv_norm_rope_cache
+    _status(lib, f(p, 3 * 256, 4, 2, 128, 1e-6, p, p, p, p, p, 256, None, 0, p, None, 4, 16, 0, 0, None),
+            1, "provided together")
+    _status(lib, f(p, 3 * 256, 4, 2, 128, 1e-6, p, p, p, p, p, 256, None, 0, p, p, 4, 16, 4, 0, None),
+            1, "slot 4 out of range")
+    _status(lib, f(p, 3 * 256, 4, 2, 128, 1e-6, p, p, p, p, p, 256, None, 0, p, p, 4, 16, 1, 13, None),
+            1, "do not fit")
+    _status(lib, f(p, 100, 4, 2, 128, 1e-6, p, p, p, p, p, 256, None, 0, None, None, 0, 0, 0, 0, None),
+            1, "row stride")

@@ -1,0 +1,143 @@
+"""GPU parity: FP8 row/column-scaled GEMM (+bias, +GELU-tanh), bit-exact where the
+result is fixed exactly, else max|err| <= 2e-2 * RMS(out) vs fp32
+dequantise-then-matmul (BASELINE tolerance) and <= 1 bf16 ulp vs the oracle's
+exact-accumulation epilogue for all but a vanishing fraction."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import DEV, announce, gen, outlier_acts, u16, u8
+from oracle import gemm as og
+from oracle import quant as oq
+from oracle.fp8 import bf16_to_f32, f32_to_bf16, f32_to_e4m3fn
+
+pytestmark = pytest.mark.gpu
+
+
+def to_dev_fp8(q_u8):
+    return torch.from_numpy(np.ascontiguousarray(q_u8)).view(torch.float8_e4m3fn).to(DEV)
+
+
+def gemm(qa_u8, qw_u8, sa, sw, bias_u16=None, out_dtype=torch.bfloat16, gelu=False):
+    import joyomni_ops as jo
+    a = to_dev_fp8(qa_u8)
+    w = to_dev_fp8(qw_u8)
+    b = None
+    if bias_u16 is not None:
+        b = torch.from_numpy(bias_u16.view(np.int16)).view(out_dtype).to(DEV)
+    fn = jo.fp8_scaled_mm_gelu_tanh if gelu else jo.fp8_scaled_mm
+    y = fn(a, w.t(), torch.from_numpy(sa).to(DEV).reshape(-1, 1),
+           torch.from_numpy(sw).to(DEV).reshape(1, -1), out_dtype, b)
+    torch.cuda.synchronize()
+    return y
+
+
+def quantized_problem(M, N, K, seed):
+    g = gen(seed)
+    x = outlier_acts(M, K, g)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    bias = (torch.randn(N, generator=g) * 0.01).to(torch.bfloat16)
+    qa, sa = oq.quant_per_token(u16(x), "bf16", "div")
+    qw, sw = oq.quant_weight_per_channel(u16(w))
+    return qa, sa, qw, sw, u16(bias)
+
+
+def assert_tolerance(y_bits, ref32, what):
+    got = bf16_to_f32(y_bits)
+    rms = float(np.sqrt(np.mean(ref32.astype(np.float64) ** 2)))
+    err = float(np.abs(got - ref32).max())
+    assert err <= 2e-2 * rms, f"{what}: max|err| {err:.3e} > 2e-2*RMS {rms:.3e}"
+
+
+def assert_ulp(y_bits, exp_bits, what, max_frac=1e-3):
+    a = y_bits.astype(np.int32)
+    b = exp_bits.astype(np.int32)
+    # bf16 patterns of same-sign values are ordered; count > 1 ulp disagreements
+    far = np.abs(a - b) > 1
+    assert np.count_nonzero(far) <= max_frac * a.size, f"{what}: {np.count_nonzero(far)} values > 1 ulp"
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 264, 256), (256, 256, 128), (33, 40, 48), (1, 8, 16),
+                                   (513, 520, 384), (64, 1024, 4096)])
+def test_exact_small_integers_bit_exact(M, N, K):
+    """fp8 integers in [-8, 8] and power-of-two scales: every partial sum is exact,
+    so the output is fixed to the last bit whatever the summation order."""
+    announce("gemm exact", M, N, K)
+    rng = np.random.default_rng(M * 7 + N)
+    qa = f32_to_e4m3fn(rng.integers(-8, 9, (M, K)).astype(np.float32))
+    qw = f32_to_e4m3fn(rng.integers(-8, 9, (N, K)).astype(np.float32))
+    sa = (2.0 ** rng.integers(-8, 2, M)).astype(np.float32)
+    sw = (2.0 ** rng.integers(-8, 2, N)).astype(np.float32)
+    bias = f32_to_bf16((rng.integers(-64, 64, N) / 16).astype(np.float32))
+    exp_bits, _ = og.scaled_mm(qa, qw, sa, sw, bias)
+    y = gemm(qa, qw, sa, sw, bias)
+    assert np.array_equal(u16(y), exp_bits)
+    exp_nb, _ = og.scaled_mm(qa, qw, sa, sw, None)
+    assert np.array_equal(u16(gemm(qa, qw, sa, sw, None)), exp_nb)
+
+
+def test_cfg0_single_linear():
+    announce("gemm cfg0 256x4096x4096")
+    qa, sa, qw, sw, bias = quantized_problem(256, 4096, 4096, 0)
+    y = u16(gemm(qa, qw, sa, sw, bias))
+    assert_tolerance(y, og.reference_fp32(qa, qw, sa, sw, bias), "cfg0")
+    exp_bits, _ = og.scaled_mm(qa, qw, sa, sw, bias)
+    assert_ulp(y, exp_bits, "cfg0")
+
+
+@pytest.mark.parametrize("K,N", [(5120, 15360), (5120, 5120), (5120, 13824), (13824, 5120)])
+def test_cfg2_full_m_sampled_rows(K, N):
+    """M=10800: every output is checked on 96 sampled rows (rows are independent)."""
+    announce("gemm cfg2 M=10800", K, N)
+    import joyomni_ops as jo
+    M = 10800
+    g = gen(K + N)
+    x = outlier_acts(M, K, g).to(DEV)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    bias = (torch.randn(N, generator=g) * 0.01).to(torch.bfloat16)
+    qa = torch.empty(M, K, dtype=torch.float8_e4m3fn, device=DEV)
+    sa = torch.empty(M, 1, device=DEV)
+    jo.per_token_quant_fp8(x, qa, sa, True)
+    qw_u8, sw = oq.quant_weight_per_channel(u16(w))
+    y = jo.fp8_scaled_mm(qa, to_dev_fp8(qw_u8).t(), sa, torch.from_numpy(sw).to(DEV).reshape(1, -1),
+                         torch.bfloat16, bias.to(DEV))
+    torch.cuda.synchronize()
+    rows = np.sort(np.random.default_rng(1).choice(M, 96, replace=False))
+    rows[-1] = M - 1  # last, partial tile row
+    ys = u16(y[torch.from_numpy(rows).to(DEV)])
+    qa_s = u8(qa[torch.from_numpy(rows).to(DEV)])
+    sa_s = sa.cpu().numpy().reshape(-1)[rows]
+    assert_tolerance(ys, og.reference_fp32(qa_s, qw_u8, sa_s, sw, u16(bias)), f"cfg2 {K}x{N}")
+    exp_bits, _ = og.scaled_mm(qa_s, qw_u8, sa_s, sw, u16(bias))
+    assert_ulp(ys, exp_bits, f"cfg2 {K}x{N}")
+
+
+@pytest.mark.parametrize("M", [64, 256, 512])
+@pytest.mark.parametrize("N", [15360, 5120])
+def test_cfg3_small_m(M, N):
+    announce("gemm cfg3", M, N)
+    qa, sa, qw, sw, bias = quantized_problem(M, N, 5120, M + N)
+    y = u16(gemm(qa, qw, sa, sw, bias))
+    # float32 torch matmul of the dequantised operands (products exact, fp32 sums)
+    a = torch.from_numpy(og.dequant(qa) * sa[:, None])
+    b = torch.from_numpy(og.dequant(qw) * sw[:, None])
+    ref = (a @ b.t()).numpy() + bf16_to_f32(bias)[None, :]
+    assert_tolerance(y, ref, f"cfg3 M={M} N={N}")
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
+def test_gelu_epilogue_and_fp16_out(out_dtype):
+    announce("gemm gelu", out_dtype)
+    qa, sa, qw, sw, bias = quantized_problem(200, 520, 512, 11)
+    bias_t = torch.from_numpy(bf16_to_f32(bias)).to(out_dtype)
+    bias_bits = bias_t.view(torch.int16).numpy().view(np.uint16)
+    plain = gemm(qa, qw, sa, sw, bias_bits, out_dtype)
+    gel = gemm(qa, qw, sa, sw, bias_bits, out_dtype, gelu=True)
+    ref = torch.nn.functional.gelu(plain.float(), approximate="tanh").to(out_dtype)
+    diff = (gel.float() - ref.float()).abs()
+    tol = (ref.float().abs() * (2.0 ** -7 if out_dtype == torch.bfloat16 else 2.0 ** -10)).clamp_min(1e-6)
+    assert bool((diff <= tol).all()), float((diff - tol).max())
+    ref32 = og.reference_fp32(qa, qw, sa, sw, bias)
+    got = plain.float().cpu().numpy()
+    rms = float(np.sqrt(np.mean(ref32.astype(np.float64) ** 2)))
+    assert np.abs(got - ref32).max() <= 2e-2 * rms

@@ -1,0 +1,38 @@
+"""GPU parity: the Fp8Linear counterpart end to end (weight quant, act quant, GEMM, GELU)."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import DEV, announce, gen, outlier_acts, u16, u8
+from oracle import gemm as og
+from oracle import quant as oq
+from oracle.fp8 import bf16_to_f32
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("gelu", [False, True])
+def test_fp8_linear_matches_oracle(gelu):
+    announce("Fp8Linear", gelu)
+    from joyomni_ops.fp8_linear import Fp8Linear, _quantize_weight_per_channel
+    g = gen(21)
+    K, N = 1024, 768
+    lin = torch.nn.Linear(K, N, bias=True)
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn(N, K, generator=g) * 0.02)
+        lin.bias.copy_(torch.randn(N, generator=g) * 0.01)
+    lin = lin.to(torch.bfloat16).to(DEV)
+    wq, ws = _quantize_weight_per_channel(lin.weight.data)
+    qw_ref, sw_ref = oq.quant_weight_per_channel(u16(lin.weight.data))
+    assert np.array_equal(u8(wq.t()), qw_ref) and np.array_equal(ws.cpu().numpy().reshape(-1), sw_ref)
+    layer = Fp8Linear.from_linear(lin, gelu_tanh=gelu)
+    x = outlier_acts(2 * 150, K, g).reshape(2, 150, K)
+    y = layer(x.to(DEV))
+    assert y.shape == (2, 150, N)
+    qa, sa = oq.quant_per_token(u16(x.reshape(-1, K)), "bf16", "div")
+    ref = og.reference_fp32(qa, qw_ref, sa, sw_ref, u16(lin.bias.data))
+    if gelu:
+        ref = og.gelu_tanh(bf16_to_f32(u16(torch.from_numpy(ref).to(torch.bfloat16))))
+    got = y.float().cpu().numpy().reshape(-1, N)
+    rms = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2)))
+    assert np.abs(got - ref).max() <= 2e-2 * rms
