@@ -69,13 +69,14 @@ def time_launches(fn, steps: int, warmup: int):
                 for _ in range(steps):
                     fn()
         torch.cuda.synchronize()
-        graph.replay()  # warm replay
-        torch.cuda.synchronize()
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        graph.replay()
-        end.record(stream)
+        with torch.cuda.stream(stream):  # replay runs on the current stream
+            graph.replay()  # warm replay
+            torch.cuda.synchronize()
+            start.record(stream)
+            graph.replay()
+            end.record(stream)
         torch.cuda.synchronize()
         return start.elapsed_time(end) / 1e3 / steps
     except Exception as exc:  # pragma: no cover - capture refused
@@ -196,6 +197,17 @@ def bench_quant(steps, warmup):
     return out
 
 
+def bench_copy(steps, warmup):
+    """Plain 1 GiB device-to-device copy: the calibration kernel for the
+    FETCH_SIZE / WRITE_SIZE counters (known 1 GiB read + 1 GiB write)."""
+    import torch
+    dev = torch.device("cuda:0")
+    src = torch.empty(1 << 29, dtype=torch.bfloat16, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    t = time_launches(lambda: dst.copy_(src), steps, warmup)
+    return {"bytes": 2 * src.numel() * 2, "us": t * 1e6, "gbs": 2 * src.numel() * 2 / t / 1e9}
+
+
 def cpu_baseline_qkv():
     """Reference CPU torch path (oracle/torch_path.py) on a bounded token sample."""
     import torch
@@ -252,7 +264,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="all", choices=["all", "qkv", "gemm", "small", "quant"])
+    ap.add_argument("--only", default="all", choices=["all", "qkv", "gemm", "small", "quant", "copy"])
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -292,6 +304,8 @@ def main():
         rec["gemm_cfg3_small_m"] = bench_small_m(args.steps, args.warmup)
     if args.only in ("all", "quant"):
         rec["act_quant"] = bench_quant(args.steps, args.warmup)
+    if args.only == "copy":
+        rec["copy"] = bench_copy(args.steps, args.warmup)
     if not args.no_cpu:
         if args.only in ("all", "qkv"):
             rec["cpu_baseline"] = cpu_baseline_qkv()

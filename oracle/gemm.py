@@ -42,6 +42,13 @@ def exact_acc(qa_u8: np.ndarray, qb_nk_u8: np.ndarray) -> np.ndarray:
     return a @ b.T
 
 
+def abs_acc(qa_u8: np.ndarray, qb_nk_u8: np.ndarray) -> np.ndarray:
+    """sum_k |A[m,k] * B[k,n]| (float64): the scale of fp32 accumulation error."""
+    a = np.abs(dequant(qa_u8).astype(np.float64))
+    b = np.abs(dequant(qb_nk_u8).astype(np.float64))
+    return a @ b.T
+
+
 def epilogue(acc: np.ndarray, sa: np.ndarray, sb: np.ndarray, bias_f32=None) -> np.ndarray:
     """fp8_gemm.cu:99-136: t = fp32(acc*sb[n]); o = fp32(t*sa[m] + bias[n]) (one fma)."""
     t = (acc.astype(np.float32) * sb.astype(np.float32)[None, :]).astype(np.float32)

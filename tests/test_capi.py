@@ -85,3 +85,13 @@ def test_norm_rope_argument_checks(lib):
             1, "do not fit")
     _status(lib, f(p, 100, 4, 2, 128, 1e-6, p, p, p, p, p, 256, None, 0, None, None, 0, 0, 0, 0, None),
             1, "row stride")
+
+
+def test_single_hip_runtime_in_process():
+    """The library must bind to the HIP runtime torch already loaded (same SONAME),
+    so its launches share torch's streams and queues."""
+    import torch  # noqa: F401
+    import joyomni_ops  # noqa: F401
+    maps = open("/proc/self/maps").read().splitlines()
+    hip = {line.split()[-1] for line in maps if "libamdhip64" in line}
+    assert len(hip) == 1, hip

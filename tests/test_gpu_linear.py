@@ -30,9 +30,14 @@ def test_fp8_linear_matches_oracle(gelu):
     y = layer(x.to(DEV))
     assert y.shape == (2, 150, N)
     qa, sa = oq.quant_per_token(u16(x.reshape(-1, K)), "bf16", "div")
-    ref = og.reference_fp32(qa, qw_ref, sa, sw_ref, u16(lin.bias.data))
-    if gelu:
-        ref = og.gelu_tanh(bf16_to_f32(u16(torch.from_numpy(ref).to(torch.bfloat16))))
+    pre = og.reference_fp32(qa, qw_ref, sa, sw_ref, u16(lin.bias.data))
+    rms = float(np.sqrt(np.mean(pre.astype(np.float64) ** 2)))
     got = y.float().cpu().numpy().reshape(-1, N)
-    rms = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2)))
-    assert np.abs(got - ref).max() <= 2e-2 * rms
+    if not gelu:
+        assert np.abs(got - pre).max() <= 2e-2 * rms
+    else:
+        # GELU is 1.13-Lipschitz: the GEMM tolerance carries over, plus the final
+        # bf16 rounding of the activation (one ulp of the result).
+        ref = og.gelu_tanh(pre)
+        ulp = np.spacing(np.abs(ref).astype(np.float32)) * 65536.0
+        assert np.all(np.abs(got - ref) <= 1.13 * 2e-2 * rms + ulp)

@@ -126,7 +126,7 @@ def test_fused_without_cache_or_k_out():
     announce("fused qkv no cache")
     import joyomni_ops as jo
     L, H, D = 40, 4, 64
-    qkv, qw, kw, cos, sin = cfg1_inputs(L, H, D, 1, 5, 8, (22, 21, 21), 10000.0, 6)
+    qkv, qw, kw, cos, sin = cfg1_inputs(L, H, D, 1, 5, 8, (24, 20, 20), 10000.0, 6)
     q_out = torch.empty(L, H, D, dtype=torch.bfloat16, device=DEV)
     jo.fused_qkv_norm_rope_cache(qkv.to(DEV), H, 1e-6, qw.to(DEV), kw.to(DEV), cos.to(DEV), sin.to(DEV),
                                  q_out, None, None, None, 0, 0)
