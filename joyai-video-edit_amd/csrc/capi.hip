@@ -30,6 +30,9 @@ joy_status hip_status(hipError_t e, const char* what) {
 
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 
+// The norm/RoPE kernel indexes (token, head) units with 32-bit integers.
+constexpr int64_t kMaxUnits = 0x7ff00000LL;
+
 }  // namespace
 
 extern "C" {
@@ -108,6 +111,7 @@ joy_status joy_fused_qk_norm_rope_3d_paired(void* q, void* k, int64_t batch, int
   if (num_heads > 0x7fffffffLL) return fail(JOY_ERR_UNSUPPORTED, "num_heads too large");
   const int64_t units = batch * seq_len * num_heads;
   if (units == 0) return ok();
+  if (units > kMaxUnits) return fail(JOY_ERR_UNSUPPORTED, "batch*seq_len*num_heads above 2^31 - 2^20");
   if (!q || !k || !q_weight || !k_weight || !cos || !sin)
     return fail(JOY_ERR_INVALID_ARGUMENT, "q, k, weights and cos/sin must be non-null");
   if (!aligned(q, 16) || !aligned(k, 16) || !aligned(q_weight, 16) || !aligned(k_weight, 16) ||
@@ -167,6 +171,8 @@ joy_status joy_fused_qkv_norm_rope_cache(const void* qkv, int64_t qkv_row_stride
                   (long long)slot_offset, (long long)(slot_offset + seq_len), (long long)slot_capacity);
   }
   if (seq_len == 0 || num_heads == 0) return ok();
+  if (seq_len * num_heads > kMaxUnits)
+    return fail(JOY_ERR_UNSUPPORTED, "seq_len*num_heads above 2^31 - 2^20");
   if (!qkv || !q_out || !q_weight || !k_weight || !cos || !sin)
     return fail(JOY_ERR_INVALID_ARGUMENT, "qkv, q_out, weights and cos/sin must be non-null");
   if ((qkv_row_stride % 8) || (q_out_stride % 8) || (k_out && (k_out_stride % 8)))

@@ -21,6 +21,8 @@
 // every load and store is a fully coalesced 128-bit access. The RMS reduction
 // runs over the D/8 lanes of a head with xor shuffles; RoPE pairs are adjacent
 // inside a lane, so rotation needs no cross-lane traffic.
+#include <stdlib.h>
+
 #include "joy_common.hpp"
 #include "joy_kernels.hpp"
 
@@ -34,9 +36,38 @@ __device__ __forceinline__ void unpack_bf16x8(const uint4& v, float f[8]) {
   f[6] = bf16_lo(v.w); f[7] = bf16_hi(v.w);
 }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// fp32 pair -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t cvt_bf16x2(float lo, float hi) {
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
 __device__ __forceinline__ uint4 pack_bf16x8(const float f[8]) {
-  return make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
-                    pack_bf16x2(f[6], f[7]));
+  return make_uint4(cvt_bf16x2(f[0], f[1]), cvt_bf16x2(f[2], f[3]), cvt_bf16x2(f[4], f[5]),
+                    cvt_bf16x2(f[6], f[7]));
+}
+
+// 16-byte global access; NT marks streaming (non-temporal) traffic.
+template <bool NT>
+__device__ __forceinline__ uint4 ld16(const uint16_t* p) {
+  if constexpr (NT) {
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+  }
+  return *(const uint4*)p;
+}
+template <bool NT>
+__device__ __forceinline__ void st16(uint16_t* p, const uint4& v) {
+  if constexpr (NT) {
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    __builtin_nontemporal_store((u32x4){v.x, v.y, v.z, v.w}, (u32x4*)p);
+  } else {
+    *(uint4*)p = v;
+  }
 }
 
 template <int LPH>
@@ -46,97 +77,128 @@ __device__ __forceinline__ float head_sum(float v) {
   return v;
 }
 
-template <int D>
-__global__ __launch_bounds__(256) void qk_norm_rope_kernel(NormRopeArgs a) {
+// UPT groups of (64 / (D/8)) consecutive (token, head) units per wave; every
+// lane issues all of its 16-byte loads before any arithmetic.
+template <int D, int UPT, bool NT>
+__global__ __launch_bounds__(512) void qk_norm_rope_kernel(NormRopeArgs a) {
   constexpr int LPH = D / 8;           // lanes per head
-  constexpr int HPW = kWave / LPH;     // heads per wave
+  constexpr int HPW = kWave / LPH;     // heads per wave per group
   const int lane = threadIdx.x & 63;
   const int li = lane % LPH;
-  const int64_t wave = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  const int64_t unit = wave * HPW + lane / LPH;  // (token, head) index
-  const int64_t units = a.n_tokens * a.num_heads;
-  const bool valid = unit < units;
-  const int64_t u = valid ? unit : units - 1;
-  const int64_t token = u / a.num_heads;
-  const int head = (int)(u - token * a.num_heads);
-  const int64_t trow = token % a.table_len;
-  const int64_t hoff = (int64_t)head * D + li * 8;
+  const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int units = (int)(a.n_tokens * a.num_heads);
 
-  const uint16_t* qi = a.q_in + token * a.in_stride + hoff;
-  const uint16_t* ki = a.k_in + token * a.in_stride + hoff;
-  uint4 qv = *(const uint4*)qi;
-  uint4 kv = *(const uint4*)ki;
-  uint4 vv = make_uint4(0, 0, 0, 0);
-  if (a.v_in) vv = *(const uint4*)(a.v_in + token * a.in_stride + hoff);
+  int token[UPT], hoff[UPT];
+  bool valid[UPT];
+  uint4 qv[UPT], kv[UPT], vv[UPT];
+  uint2 cv[UPT], sv[UPT];
+#pragma unroll
+  for (int r = 0; r < UPT; ++r) {
+    const int unit = (wave * UPT + r) * HPW + lane / LPH;
+    valid[r] = unit < units;
+    const int u = valid[r] ? unit : units - 1;
+    token[r] = u / a.num_heads;
+    hoff[r] = (u - token[r] * a.num_heads) * D + li * 8;
+    const int64_t in = (int64_t)token[r] * a.in_stride + hoff[r];
+    qv[r] = ld16<NT>(a.q_in + in);
+    kv[r] = ld16<NT>(a.k_in + in);
+    if (a.v_in) vv[r] = ld16<NT>(a.v_in + in);
+    const int64_t trow = (int64_t)(token[r] % a.table_len) * (D / 2) + li * 4;
+    cv[r] = *(const uint2*)(a.cos + trow);
+    sv[r] = *(const uint2*)(a.sin + trow);
+  }
   const uint4 qwv = *(const uint4*)(a.q_weight + li * 8);
   const uint4 kwv = *(const uint4*)(a.k_weight + li * 8);
-  const uint2 cv = *(const uint2*)(a.cos + trow * (D / 2) + li * 4);
-  const uint2 sv = *(const uint2*)(a.sin + trow * (D / 2) + li * 4);
-
-  float q[8], k[8], qw[8], kw[8];
-  unpack_bf16x8(qv, q);
-  unpack_bf16x8(kv, k);
+  float qw[8], kw[8];
   unpack_bf16x8(qwv, qw);
   unpack_bf16x8(kwv, kw);
-  const float c[4] = {bf16_lo(cv.x), bf16_hi(cv.x), bf16_lo(cv.y), bf16_hi(cv.y)};
-  const float s[4] = {bf16_lo(sv.x), bf16_hi(sv.x), bf16_lo(sv.y), bf16_hi(sv.y)};
-
-  float ssq = 0.f, ssk = 0.f;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    ssq = __builtin_fmaf(q[j], q[j], ssq);
-    ssk = __builtin_fmaf(k[j], k[j], ssk);
-  }
-  ssq = head_sum<LPH>(ssq);
-  ssk = head_sum<LPH>(ssk);
   const float inv_d = 1.0f / (float)D;
-  const float rq = __builtin_amdgcn_rsqf(ssq * inv_d + a.eps);
-  const float rk = __builtin_amdgcn_rsqf(ssk * inv_d + a.eps);
 
-  float qo[8], ko[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    q[j] = q[j] * rq * qw[j];
-    k[j] = k[j] * rk * kw[j];
-  }
+  for (int r = 0; r < UPT; ++r) {
+    float q[8], k[8];
+    unpack_bf16x8(qv[r], q);
+    unpack_bf16x8(kv[r], k);
+    const float c[4] = {bf16_lo(cv[r].x), bf16_hi(cv[r].x), bf16_lo(cv[r].y), bf16_hi(cv[r].y)};
+    const float s[4] = {bf16_lo(sv[r].x), bf16_hi(sv[r].x), bf16_lo(sv[r].y), bf16_hi(sv[r].y)};
+    float ssq = 0.f, ssk = 0.f;
 #pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    qo[2 * p] = q[2 * p] * c[p] - q[2 * p + 1] * s[p];
-    qo[2 * p + 1] = q[2 * p] * s[p] + q[2 * p + 1] * c[p];
-    ko[2 * p] = k[2 * p] * c[p] - k[2 * p + 1] * s[p];
-    ko[2 * p + 1] = k[2 * p] * s[p] + k[2 * p + 1] * c[p];
+    for (int j = 0; j < 8; ++j) {
+      ssq = __builtin_fmaf(q[j], q[j], ssq);
+      ssk = __builtin_fmaf(k[j], k[j], ssk);
+    }
+    ssq = head_sum<LPH>(ssq);
+    ssk = head_sum<LPH>(ssk);
+    const float rq = __builtin_amdgcn_rsqf(ssq * inv_d + a.eps);
+    const float rk = __builtin_amdgcn_rsqf(ssk * inv_d + a.eps);
+    float qo[8], ko[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      q[j] = q[j] * rq * qw[j];
+      k[j] = k[j] * rk * kw[j];
+    }
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      qo[2 * p] = q[2 * p] * c[p] - q[2 * p + 1] * s[p];
+      qo[2 * p + 1] = q[2 * p] * s[p] + q[2 * p + 1] * c[p];
+      ko[2 * p] = k[2 * p] * c[p] - k[2 * p + 1] * s[p];
+      ko[2 * p + 1] = k[2 * p] * s[p] + k[2 * p + 1] * c[p];
+    }
+    if (!valid[r]) continue;
+    const int64_t t = token[r];
+    st16<NT>(a.q_out + t * a.q_out_stride + hoff[r], pack_bf16x8(qo));
+    if (a.k_out) st16<NT>(a.k_out + t * a.k_out_stride + hoff[r], pack_bf16x8(ko));
+    if (a.kpre_out) st16<NT>(a.kpre_out + t * a.kpre_stride + hoff[r], pack_bf16x8(k));
+    if (a.v_out) st16<NT>(a.v_out + t * a.v_out_stride + hoff[r], vv[r]);
   }
-  if (!valid) return;
-  *(uint4*)(a.q_out + token * a.q_out_stride + hoff) = pack_bf16x8(qo);
-  if (a.k_out) *(uint4*)(a.k_out + token * a.k_out_stride + hoff) = pack_bf16x8(ko);
-  if (a.kpre_out) *(uint4*)(a.kpre_out + token * a.kpre_stride + hoff) = pack_bf16x8(k);
-  if (a.v_out) *(uint4*)(a.v_out + token * a.v_out_stride + hoff) = vv;
+}
+
+// Tuning switches while the launch shape is evaluated: JOY_QKV_CFG = UPT*100 + NT*10 + waves/4.
+int qkv_cfg() {
+  static const int v = [] {
+    const char* e = getenv("JOY_QKV_CFG");
+    return e ? atoi(e) : 112;
+  }();
+  return v;
+}
+
+template <int D, int UPT, bool NT>
+hipError_t launch_norm_rope(const NormRopeArgs& a, hipStream_t st, int wpb) {
+  const int64_t units = a.n_tokens * a.num_heads;
+  constexpr int HPW = kWave / (D / 8);
+  const int64_t waves = (units + HPW * UPT - 1) / (HPW * UPT);
+  hipLaunchKernelGGL((qk_norm_rope_kernel<D, UPT, NT>), dim3((unsigned)((waves + wpb - 1) / wpb)),
+                     dim3(wpb * kWave), 0, st, a);
+  return hipGetLastError();
+}
+
+template <int D>
+hipError_t launch_norm_rope_d(const NormRopeArgs& a, hipStream_t st) {
+  const int cfg = qkv_cfg();
+  const int wpb = (cfg % 10) == 2 ? 8 : 4;
+  const bool nt = (cfg / 10) % 10 == 1;
+  switch (cfg / 100) {
+    case 2:
+      return nt ? launch_norm_rope<D, 2, true>(a, st, wpb) : launch_norm_rope<D, 2, false>(a, st, wpb);
+    default:
+      return nt ? launch_norm_rope<D, 1, true>(a, st, wpb) : launch_norm_rope<D, 1, false>(a, st, wpb);
+  }
 }
 
 }  // namespace
 
 hipError_t launch_qk_norm_rope(const NormRopeArgs& a, int head_dim, hipStream_t st) {
-  const int64_t units = a.n_tokens * a.num_heads;
-  if (units == 0) return hipSuccess;
-  const int hpw = kWave / (head_dim / 8);
-  const int64_t waves = (units + hpw - 1) / hpw;
-  const int wpb = 4;
-  const dim3 grid((unsigned)((waves + wpb - 1) / wpb));
-  const dim3 block(wpb * kWave);
+  if (a.n_tokens * a.num_heads == 0) return hipSuccess;
   switch (head_dim) {
     case 64:
-      hipLaunchKernelGGL(qk_norm_rope_kernel<64>, grid, block, 0, st, a);
-      break;
+      return launch_norm_rope_d<64>(a, st);
     case 128:
-      hipLaunchKernelGGL(qk_norm_rope_kernel<128>, grid, block, 0, st, a);
-      break;
+      return launch_norm_rope_d<128>(a, st);
     case 256:
-      hipLaunchKernelGGL(qk_norm_rope_kernel<256>, grid, block, 0, st, a);
-      break;
+      return launch_norm_rope_d<256>(a, st);
     default:
       return hipErrorInvalidValue;
   }
-  return hipGetLastError();
 }
 
 }  // namespace joy

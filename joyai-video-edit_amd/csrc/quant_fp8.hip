@@ -87,6 +87,19 @@ __device__ __forceinline__ float scale_value(float x, float s, float r) {
   return x * r;
 }
 
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+
+// Streaming (non-temporal) 16-byte load / 8-byte store: rows are read and
+// written exactly once.
+__device__ __forceinline__ uint4 ld_stream(const uint4* p) {
+  const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ void st_stream(uint2* p, const uint2& v) {
+  __builtin_nontemporal_store((u32x2){v.x, v.y}, (u32x2*)p);
+}
+
 // VPT = 16-byte vectors per lane (row length K = 8 * nvec, nvec <= 64 * VPT).
 template <bool kFp16, bool kDivide, int VPT>
 __global__ __launch_bounds__(256) void quant_rows_vec(const uint4* __restrict__ in,
@@ -103,7 +116,7 @@ __global__ __launch_bounds__(256) void quant_rows_vec(const uint4* __restrict__ 
   for (int i = 0; i < VPT; ++i) {
     const int idx = lane + i * kWave;
     if (idx < nvec) {
-      v[i] = src[idx];
+      v[i] = ld_stream(&src[idx]);
     } else {
       v[i] = make_uint4(0, 0, 0, 0);
     }
@@ -133,7 +146,7 @@ __global__ __launch_bounds__(256) void quant_rows_vec(const uint4* __restrict__ 
         uint2 o;
         o.x = pack_fp8x4(f[0], f[1], f[2], f[3]);
         o.y = pack_fp8x4(f[4], f[5], f[6], f[7]);
-        dst[idx] = o;
+        st_stream(&dst[idx], o);
       }
     }
   } else {
