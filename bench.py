@@ -49,6 +49,9 @@ def quant_bytes(M, K) -> int:
     return 2 * M * K + M * K + 4 * M
 
 
+EAGER = False  # --eager: plain launches instead of one HIP graph (for counter runs)
+
+
 def time_launches(fn, steps: int, warmup: int):
     """Average per-launch time (s) of `fn` (one kernel launch) over `steps` launches.
 
@@ -61,6 +64,8 @@ def time_launches(fn, steps: int, warmup: int):
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    if EAGER:
+        return _time_eager(fn, steps)
     stream = torch.cuda.Stream()
     graph = torch.cuda.CUDAGraph()
     try:
@@ -81,6 +86,11 @@ def time_launches(fn, steps: int, warmup: int):
         return start.elapsed_time(end) / 1e3 / steps
     except Exception as exc:  # pragma: no cover - capture refused
         print(f"bench: graph capture failed ({exc!r}); timing eager launches", file=sys.stderr)
+    return _time_eager(fn, steps)
+
+
+def _time_eager(fn, steps: int):
+    import torch
     stream = torch.cuda.current_stream()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
@@ -146,13 +156,27 @@ def bench_gemm(steps, warmup):
         fn = jo.fp8_scaled_mm_gelu_tanh if name == "ffn_up" else jo.fp8_scaled_mm
         t = time_launches(lambda: fn(qa, wt, sa, swr, torch.bfloat16, bias), steps, warmup)
         flops = 2 * M * N * K
-        res.append({"shape": name, "M": M, "K": K, "N": N, "ms": t * 1e3,
-                    "tflops": flops / t / 1e12, "frac_fp8_peak": flops / t / 1e12 / PEAK_FP8_TFLOPS,
-                    "epilogue": "bias+gelu_tanh" if name == "ffn_up" else "bias"})
+        rec = {"shape": name, "M": M, "K": K, "N": N, "ms": t * 1e3,
+               "tflops": flops / t / 1e12, "frac_fp8_peak": flops / t / 1e12 / PEAK_FP8_TFLOPS,
+               "epilogue": "bias+gelu_tanh" if name == "ffn_up" else "bias"}
+        # the reference's own ROCm GEMM call (fp8_linear.py:124-132 -> hipBLASLt), same inputs
+        try:
+            tr = time_launches(lambda: torch._scaled_mm(qa, wt, scale_a=sa, scale_b=swr, bias=bias,
+                                                        out_dtype=torch.bfloat16, use_fast_accum=True),
+                               steps, warmup)
+            rec["reference_hipblaslt_tflops"] = flops / tr / 1e12
+            rec["speedup_vs_reference_gpu"] = tr / t
+        except Exception as exc:  # pragma: no cover - depends on the torch build
+            rec["reference_hipblaslt_tflops"] = None
+            rec["reference_hipblaslt_error"] = str(exc)[:200]
+        res.append(rec)
         del x, w, qa, qw
     tot_flops = sum(2 * r["M"] * r["N"] * r["K"] for r in res)
     tot_t = sum(r["ms"] for r in res) / 1e3
-    return res, tot_flops / tot_t / 1e12
+    ref_t = [2 * r["M"] * r["N"] * r["K"] / r["reference_hipblaslt_tflops"] / 1e12
+             for r in res if r.get("reference_hipblaslt_tflops")]
+    ref_agg = tot_flops / sum(ref_t) / 1e12 if len(ref_t) == len(res) else None
+    return res, tot_flops / tot_t / 1e12, ref_agg
 
 
 def bench_small_m(steps, warmup):
@@ -264,8 +288,11 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--eager", action="store_true", help="time plain launches (no HIP graph)")
     ap.add_argument("--only", default="all", choices=["all", "qkv", "gemm", "small", "quant", "copy"])
     args = ap.parse_args()
+    global EAGER
+    EAGER = args.eager
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
               "the hot path has no multi-GPU component in this tier.", file=sys.stderr)
@@ -291,9 +318,10 @@ def main():
                            "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": load_traffic("qkv_norm_rope"),
                            "algorithmic_bytes": b, "kernel": "qk_norm_rope_kernel<128>"}
     if args.only in ("all", "gemm"):
-        res, agg = bench_gemm(max(5, args.steps // 5), max(2, args.warmup // 2))
+        res, agg, ref_agg = bench_gemm(max(5, args.steps // 5), max(2, args.warmup // 2))
         best = max(res, key=lambda r: r["tflops"])
         rec["gemm_cfg2"] = {"shapes": res, "aggregate_tflops": round(agg, 1),
+                            "reference_hipblaslt_aggregate_tflops": round(ref_agg, 1) if ref_agg else None,
                             "roofline": {"bound": "mfma", "achieved": round(agg, 1), "peak": PEAK_FP8_TFLOPS,
                                          "unit": "TFLOP/s", "frac": round(agg / PEAK_FP8_TFLOPS, 4),
                                          "traffic": load_traffic("fp8_gemm_qkv"),

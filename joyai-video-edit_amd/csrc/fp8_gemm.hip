@@ -9,24 +9,24 @@
 // applies F.gelu(approximate="tanh") to the rounded output, as the reference
 // model does after its up-projection (deploy/xvideo/models/dit/dit.py:87-89).
 //
-// Large-M kernel (MFMA-bound):
-//  * macro tile 256x256, K step 128 bytes, 256 threads = 4 waves in 2x2, each
-//    wave owns a 128x128 sub-tile as 4x4 v_mfma_f32_32x32x64_f8f6f4 tiles
-//    (256 fp32 accumulators per lane, held in AGPR/VGPR);
-//  * both operands are K-contiguous, so a lane's MFMA fragment (32 K-bytes of
-//    one row) is two 16-byte LDS reads. The MFMA takes W as its "A" operand and
-//    the activation as "B", so each lane ends with 4 consecutive output columns
-//    of one output row -> 8-byte stores;
-//  * global -> LDS with gfx950 16-byte direct-to-LDS loads
-//    (global_load_lds_dwordx4), double-buffered in two static LDS halves
-//    (128 KiB of the 160 KiB), one barrier per K step;
-//  * LDS rows are 128 bytes = 8 chunks of 16 bytes; chunk c of row r is stored at
-//    c ^ swz(r), swz(r) = (r & 7) ^ ((r >> 3) & 1), which makes both the
-//    direct-to-LDS writes and the fragment reads bank-conflict free for 8- and
-//    16-lane service groups;
-//  * blockIdx -> tile mapping is XCD-aware (consecutive workgroups land on
-//    different XCDs, so each XCD gets a contiguous tile range) and grouped
-//    (GROUP_M tile-rows share B columns in one XCD's L2).
+// Main kernel (fp8_gemm_4w, any M, N with K % 64 == 0):
+//  * 256 threads = 4 waves in 2x2, one wave per SIMD; macro tile 256x256 for the
+//    full rounds of the grid (one workgroup per CU), 256x128 or 128x128 sub-tiles
+//    for the tiles of the last, partial round, so more CUs share it;
+//  * each wave accumulates its sub-tile as 32x32 tiles of
+//    v_mfma_f32_32x32x64_f8f6f4 (up to 256 fp32 accumulators per lane, AGPRs);
+//    the MFMA takes W as its "A" operand and the activation as "B";
+//  * both operands are K-contiguous; they reach LDS with gfx950 16-byte
+//    direct-to-LDS loads (global_load_lds_dwordx4) into a 5-deep ring of 64-byte
+//    K steps, one barrier per step, with fragments of the next step read into a
+//    second register set while the current step's MFMAs run;
+//  * the epilogue rounds the tile into LDS and writes whole row segments with
+//    16-byte stores;
+//  * blockIdx -> tile mapping is XCD-aware (each XCD gets a contiguous range of
+//    tile positions) and grouped (4 tile rows walk the tile columns together,
+//    so one XCD's L2 serves both operands).
+// A one-wave-per-32x32-tile kernel straight from global memory covers every
+// other shape with K % 16 == 0.
 #include <stdlib.h>
 
 #include "joy_common.hpp"
@@ -35,26 +35,13 @@
 namespace joy {
 namespace {
 
-constexpr int BK = 128;
-#ifndef JOY_BM
-#define JOY_BM 256
-#define JOY_BN 256
-#define JOY_WM 2
-#define JOY_WN 4
-#endif
+constexpr int kGroupM = 4;  // tile rows per group of the tile order
 
 typedef __attribute__((address_space(3))) void lds_void;
-
-__device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
 __device__ __forceinline__ v16f mfma_32x32x64_fp8(const v8i& a, const v8i& b, const v16f& c) {
   // Scale operands of zero select the plain (unscaled) f8f6f4 MFMA; format 0 = e4m3.
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
-}
-
-__device__ __forceinline__ void wait_vmem_all() {
-  // s_waitcnt vmcnt(0): gfx9 encoding, expcnt and lgkmcnt left at their maxima.
-  __builtin_amdgcn_s_waitcnt(0x0f70);
 }
 
 // GELU, tanh form: 0.5 x (1 + tanh(u)) == x * sigmoid(2u), u = sqrt(2/pi) (x + 0.044715 x^3).
@@ -91,49 +78,55 @@ __device__ __forceinline__ float unpack_hi(uint32_t w) {
   return fp16_bits_to_f32(w >> 16);
 }
 
-// Epilogue of one wave's FN x FM grid of 32x32 MFMA tiles. acc[i][j][r] holds
-// output row m_base + 32j + (lane % 32) and column n_base + 32i + 8(r/4) + 4g + r%4.
-// Column operands (scale, bias) are loaded once per lane up front, then every
-// output quad is rounded, optionally passed through GELU, and stored as 8 bytes.
-template <bool kBf16, bool kGelu, int FN, int FM>
-__device__ __forceinline__ void store_tile(const v16f (&acc)[FN][FM], int m_base, int n_base,
-                                           int frow, int g, const float* __restrict__ sa,
-                                           const float* __restrict__ sb,
-                                           const uint16_t* __restrict__ bias,
-                                           uint16_t* __restrict__ C, int M, int N, int64_t ldc) {
-  float4 sbv[FN][4];
-  uint2 bv[FN][4];
+// Column operands of one wave's 128-column slice, loaded once per tile (ahead of
+// the main loop, so their latency is hidden): scales_b and bias for the four
+// consecutive output columns n_base + 32i + 8q + 4g of every accumulator quad.
+template <int FN>
+struct ColOperands {
+  float4 sb[FN][4];
+  uint2 bias[FN][4];
+};
+
+template <int FN>
+__device__ __forceinline__ void load_col_operands(ColOperands<FN>& c, int n_base, int g, int N,
+                                                  const float* __restrict__ sb,
+                                                  const uint16_t* __restrict__ bias) {
 #pragma unroll
   for (int i = 0; i < FN; ++i)
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int n = n_base + i * 32 + q * 8 + g * 4;
       const bool ok = n < N;
-      sbv[i][q] = ok ? *(const float4*)(sb + n) : make_float4(0.f, 0.f, 0.f, 0.f);
-      bv[i][q] = (ok && bias) ? *(const uint2*)(bias + n) : make_uint2(0u, 0u);
+      c.sb[i][q] = ok ? *(const float4*)(sb + n) : make_float4(0.f, 0.f, 0.f, 0.f);
+      c.bias[i][q] = (ok && bias) ? *(const uint2*)(bias + n) : make_uint2(0u, 0u);
     }
-  float sav[FM];
+}
+
+// Epilogue through LDS: the wave's (32*FN) x (32*FM) tile is rounded to 16-bit, written
+// to a private LDS staging area [32*FM rows][32*FN columns] with a row pitch of
+// 32*FN*2 + 16 bytes (16 lanes x 16 bytes cover all banks once for the 8-byte writes
+// and for the 16-byte reads), then read back row-wise so that each global store
+// instruction writes 64 x 16 contiguous bytes (whole row segments).
+template <bool kBf16, bool kGelu, int FN, int FM>
+__device__ __forceinline__ void store_tile_lds(const v16f (&acc)[FN][FM], const ColOperands<FN>& col,
+                                               const float (&sav)[FM], uint8_t* stage, int m_base,
+                                               int n_base, int lane, uint16_t* __restrict__ C,
+                                               int M, int N, int64_t ldc) {
+  constexpr int ROW_BYTES = 32 * FN * 2;
+  constexpr int PITCH = ROW_BYTES + 16;
+  const int frow = lane & 31, g = lane >> 5;
 #pragma unroll
   for (int j = 0; j < FM; ++j) {
-    const int m = m_base + j * 32 + frow;
-    sav[j] = m < M ? sa[m] : 0.0f;
-  }
-  // interior wave tiles (all but the last tile row/column) store without guards
-  const bool interior = (m_base + 32 * FM <= M) && (n_base + 32 * FN <= N);
+    uint8_t* srow = stage + (j * 32 + frow) * PITCH;
 #pragma unroll
-  for (int j = 0; j < FM; ++j) {
-    const int m = m_base + j * 32 + frow;
-    if (!interior && m >= M) continue;
-    uint16_t* crow = C + (int64_t)m * ldc;
-#pragma unroll
-    for (int i = 0; i < FN; ++i) {
+    for (int i = 0; i < FN; ++i)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int n = n_base + i * 32 + q * 8 + g * 4;
-        if (!interior && n >= N) continue;
-        const float sbe[4] = {sbv[i][q].x, sbv[i][q].y, sbv[i][q].z, sbv[i][q].w};
-        const float be[4] = {unpack_lo<kBf16>(bv[i][q].x), unpack_hi<kBf16>(bv[i][q].x),
-                             unpack_lo<kBf16>(bv[i][q].y), unpack_hi<kBf16>(bv[i][q].y)};
+        const float4 s = col.sb[i][q];
+        const uint2 bb = col.bias[i][q];
+        const float sbe[4] = {s.x, s.y, s.z, s.w};
+        const float be[4] = {unpack_lo<kBf16>(bb.x), unpack_hi<kBf16>(bb.x), unpack_lo<kBf16>(bb.y),
+                             unpack_hi<kBf16>(bb.y)};
         float o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) o[e] = __builtin_fmaf(acc[i][j][q * 4 + e] * sbe[e], sav[j], be[e]);
@@ -143,9 +136,20 @@ __device__ __forceinline__ void store_tile(const v16f (&acc)[FN][FM], int m_base
           pk = make_uint2(pack2<kBf16>(gelu_tanh(unpack_lo<kBf16>(pk.x)), gelu_tanh(unpack_hi<kBf16>(pk.x))),
                           pack2<kBf16>(gelu_tanh(unpack_lo<kBf16>(pk.y)), gelu_tanh(unpack_hi<kBf16>(pk.y))));
         }
-        *(uint2*)(crow + n) = pk;
+        *(uint2*)(srow + (i * 32 + q * 8 + g * 4) * 2) = pk;
       }
-    }
+  }
+  // read back: CPL lanes per row, 64/CPL rows per instruction
+  constexpr int CPL = ROW_BYTES / 16;
+  constexpr int RPI = 64 / CPL;
+  const int rr = lane / CPL, cc = lane % CPL;
+  const int n = n_base + cc * 8;
+#pragma unroll
+  for (int r0 = 0; r0 < 32 * FM; r0 += RPI) {
+    const int r = r0 + rr;
+    const uint4 v = *(const uint4*)(stage + r * PITCH + cc * 16);
+    const int m = m_base + r;
+    if (m < M && n < N) *(uint4*)(C + (int64_t)m * ldc + n) = v;
   }
 }
 
@@ -166,144 +170,31 @@ struct TileCoord {
   int tm, tn;
 };
 
-__device__ __forceinline__ TileCoord map_tile(int b, int tiles_m, int tiles_n, int group_m) {
-  const int T = tiles_m * tiles_n;
-  // XCD-aware: hardware deals workgroups round-robin to the 8 XCDs.
-  const int xcd = b & 7, local = b >> 3, q = T >> 3, rem = T & 7;
-  const int t = xcd < rem ? xcd * (q + 1) + local : rem * (q + 1) + (xcd - rem) * q + local;
+__device__ __forceinline__ TileCoord map_tile(int b, int nblocks, int tiles_m, int tiles_n,
+                                              int group_m, int base) {
+  int t = b;
+  if (nblocks > 0) {
+    // XCD-aware: hardware deals workgroups round-robin to the 8 XCDs; give each XCD
+    // a contiguous range of positions so its L2 sees neighbouring tiles.
+    const int xcd = b & 7, local = b >> 3, q = nblocks >> 3, rem = nblocks & 7;
+    t = xcd < rem ? xcd * (q + 1) + local : rem * (q + 1) + (xcd - rem) * q + local;
+  }
+  t += base;
+  // grouped order: group_m tile rows walk the tile columns together
   const int per_group = group_m * tiles_n;
-  const int g = t / per_group;
-  const int first_m = g * group_m;
+  const int grp = t / per_group;
+  const int first_m = grp * group_m;
   const int gsz = min(tiles_m - first_m, group_m);
-  const int r = t - g * per_group;
+  const int r = t - grp * per_group;
   return {first_m + r % gsz, r / gsz};
 }
 
-template <bool kBf16, bool kGelu, int BM, int BN, int WAVES_M, int WAVES_N>
-__global__ __launch_bounds__(WAVES_M * WAVES_N * 64, 1) void fp8_gemm_tiled(
-    const uint8_t* __restrict__ A, const uint8_t* __restrict__ W, const float* __restrict__ sa,
-    const float* __restrict__ sb, const uint16_t* __restrict__ bias, uint16_t* __restrict__ C,
-    int M, int N, int K, int64_t ldc, int tiles_m, int tiles_n, int group_m) {
-  constexpr int NW = WAVES_M * WAVES_N;      // waves per workgroup
-  constexpr int WTM = BM / WAVES_M;          // wave tile rows (activation rows)
-  constexpr int WTN = BN / WAVES_N;          // wave tile cols (weight rows)
-  constexpr int FM = WTM / 32, FN = WTN / 32;
-  constexpr int IA = BM / 8 / NW, IW = BN / 8 / NW;  // 8-row load instructions per wave
-  static_assert(IA * 8 * NW == BM && IW * 8 * NW == BN, "tile rows must split over waves");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds_a0[BM * BK];
-  __shared__ __attribute__((aligned(1024))) uint8_t lds_w0[BN * BK];
-  __shared__ __attribute__((aligned(1024))) uint8_t lds_a1[BM * BK];
-  __shared__ __attribute__((aligned(1024))) uint8_t lds_w1[BN * BK];
-
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const TileCoord tc = map_tile(blockIdx.x, tiles_m, tiles_n, group_m);
-  const int m0 = tc.tm * BM, n0 = tc.tn * BN;
-
-  // ---- global -> LDS addressing: wave w fills rows [w*IA*8, (w+1)*IA*8) of
-  // the activation tile (and likewise for W) with 8-row x 128-byte instructions.
-  const int lrow = lane >> 3;   // row within an 8-row instruction
-  const int lchunk = lane & 7;  // physical 16-byte chunk this lane writes
-  int64_t ga[IA], gw[IW];
-#pragma unroll
-  for (int i = 0; i < IA; ++i) {
-    const int row = (wave * IA + i) * 8 + lrow;
-    const int c = lchunk ^ swz(row);  // logical chunk whose bytes land here
-    ga[i] = (int64_t)min(m0 + row, M - 1) * K + c * 16;
-  }
-#pragma unroll
-  for (int i = 0; i < IW; ++i) {
-    const int row = (wave * IW + i) * 8 + lrow;
-    const int c = lchunk ^ swz(row);
-    gw[i] = (int64_t)min(n0 + row, N - 1) * K + c * 16;
-  }
-  auto issue = [&](uint8_t* la, uint8_t* lw, int kt) {
-    const int64_t koff = (int64_t)kt * BK;
-#pragma unroll
-    for (int i = 0; i < IA; ++i)
-      __builtin_amdgcn_global_load_lds((const void*)(A + ga[i] + koff),
-                                       (lds_void*)(la + (wave * IA + i) * 8 * BK), 16, 0, 0);
-#pragma unroll
-    for (int i = 0; i < IW; ++i)
-      __builtin_amdgcn_global_load_lds((const void*)(W + gw[i] + koff),
-                                       (lds_void*)(lw + (wave * IW + i) * 8 * BK), 16, 0, 0);
-  };
-
-  // ---- fragment addressing: wave (wm, wn) owns activation rows [WTM*wm, +WTM)
-  // and weight rows [WTN*wn, +WTN). A lane reads row (l % 32) of a 32-row
-  // fragment, K bytes [32g, 32g+32) of the 64-byte MFMA step, g = l / 32.
-  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
-  const int frow = lane & 31, g = lane >> 5;
-  // All fragment rows are frow + 32*f (+ multiples of 32), so swz(row) == swz(frow).
-  const int sw = swz(frow);
-  const int off00 = ((0 + g * 2) ^ sw) * 16, off01 = ((1 + g * 2) ^ sw) * 16;
-  const int off10 = ((4 + g * 2) ^ sw) * 16, off11 = ((5 + g * 2) ^ sw) * 16;
-  v16f acc[FN][FM];  // [weight-fragment][activation-fragment]
-#pragma unroll
-  for (int i = 0; i < FN; ++i)
-#pragma unroll
-    for (int j = 0; j < FM; ++j) acc[i][j] = (v16f){};
-
-  auto compute = [&](const uint8_t* la, const uint8_t* lw) {
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const int o0 = kk ? off10 : off00, o1 = kk ? off11 : off01;
-      v8i fw[FN], fa[FM];
-#pragma unroll
-      for (int f = 0; f < FN; ++f) {
-        const uint8_t* rw = lw + (wn * WTN + f * 32 + frow) * BK;
-        const v4i lo = *(const v4i*)(rw + o0);
-        const v4i hi = *(const v4i*)(rw + o1);
-        fw[f] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-      }
-#pragma unroll
-      for (int f = 0; f < FM; ++f) {
-        const uint8_t* ra = la + (wm * WTM + f * 32 + frow) * BK;
-        const v4i lo = *(const v4i*)(ra + o0);
-        const v4i hi = *(const v4i*)(ra + o1);
-        fa[f] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-      }
-#pragma unroll
-      for (int i = 0; i < FN; ++i)
-#pragma unroll
-        for (int j = 0; j < FM; ++j) acc[i][j] = mfma_32x32x64_fp8(fw[i], fa[j], acc[i][j]);
-    }
-  };
-
-  // Single-exit loop over pairs of K steps (buffer 0 then buffer 1), so the
-  // accumulators stay in place across iterations; an odd last step follows.
-  const int nk = K / BK;
-  issue(lds_a0, lds_w0, 0);
-  wait_vmem_all();
-  __syncthreads();
-  for (int kt = 0; kt + 1 < nk; kt += 2) {
-    issue(lds_a1, lds_w1, kt + 1);
-    compute(lds_a0, lds_w0);
-    wait_vmem_all();
-    __syncthreads();
-    if (kt + 2 < nk) issue(lds_a0, lds_w0, kt + 2);
-    compute(lds_a1, lds_w1);
-    wait_vmem_all();
-    __syncthreads();
-  }
-  if (nk & 1) compute(lds_a0, lds_w0);
-
-  store_tile<kBf16, kGelu, FN, FM>(acc, m0 + wm * WTM, n0 + wn * WTN, frow, g, sa, sb, bias, C, M, N, ldc);
-}
-
-// ---------------------------------------------------------------------------
-// Pipelined large-M kernel: K step KS bytes (64 or 128), STAGES-deep ring of LDS
-// slots fed by direct-to-LDS loads issued STAGES-1 steps ahead, one barrier per
-// step.
-//
-// LDS rows are KS bytes = KS/16 chunks of 16 bytes; logical chunk c of row r is
-// stored at c ^ swz(r). Both swizzles were chosen by measuring
-// SQ_LDS_BANK_CONFLICT on gfx950 (zero for the fragment reads below):
+// LDS rows of the operand ring are KS bytes = KS/16 chunks of 16 bytes; logical
+// chunk c of row r is stored at c ^ swz(r). Both swizzles were chosen by measuring
+// SQ_LDS_BANK_CONFLICT on gfx950 (zero for the fragment reads):
 //   KS = 64:  swz(r) = (r >> 2) & 3
 //   KS = 128: swz(r) = (r & 7) ^ ((r >> 3) & 1)
 // Both are invariant under r -> r + 32, so a lane's fragment rows share its swizzle.
-// With KS = 128 every DMA instruction moves whole 128-byte lines (8 rows x 128 B).
-// ---------------------------------------------------------------------------
 template <int KS>
 __device__ __forceinline__ int swz_rows(int r) {
   if constexpr (KS == 64) return (r >> 2) & 3;
@@ -321,149 +212,6 @@ __device__ __forceinline__ void block_barrier() {
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-}
-
-template <bool kBf16, bool kGelu, int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int KS,
-          int TOUCH>
-__global__ __launch_bounds__(WAVES_M * WAVES_N * 64, 1) void fp8_gemm_pipe(
-    const uint8_t* __restrict__ A, const uint8_t* __restrict__ W, const float* __restrict__ sa,
-    const float* __restrict__ sb, const uint16_t* __restrict__ bias, uint16_t* __restrict__ C,
-    int M, int N, int K, int64_t ldc, int tiles_m, int tiles_n, int group_m) {
-  constexpr int NW = WAVES_M * WAVES_N;
-  constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
-  constexpr int FM = WTM / 32, FN = WTN / 32;
-  constexpr int CPR = KS / 16;                        // 16-byte chunks per row
-  constexpr int RPI = 64 / CPR;                       // rows per DMA instruction
-  constexpr int IA = BM / RPI / NW, IW = BN / RPI / NW;  // DMA instructions per wave
-  constexpr int LOADS = IA + IW;                      // per wave per stage
-  constexpr int A_BYTES = BM * KS, SLOT = (BM + BN) * KS;
-  static_assert(KS == 64 || KS == 128, "K step");
-  static_assert(IA * RPI * NW == BM && IW * RPI * NW == BN, "tile rows must split over waves");
-  // TOUCH > 0: every lane also pulls one 128-byte line of the stage TOUCH steps
-  // beyond the newest DMA stage into L2 (4-byte load into a scratch LDS area), so
-  // the DMA for that stage later hits L2. One extra load per wave per step.
-  constexpr int TPL = (BM + BN + NW * 64 - 1) / (NW * 64);  // touched rows per lane
-  constexpr int TLOADS = TOUCH ? TPL : 0;
-  constexpr int PER_STEP = LOADS + TLOADS;
-  static_assert((STAGES - 2) * PER_STEP + TLOADS < 64, "vmcnt range");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[STAGES * SLOT + (TOUCH ? 256 * NW : 0)];
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const TileCoord tc = map_tile(blockIdx.x, tiles_m, tiles_n, group_m);
-  const int m0 = tc.tm * BM, n0 = tc.tn * BN;
-
-  // DMA addressing: lane l of an instruction writes row l / CPR, physical chunk l % CPR.
-  const int lrow = lane / CPR, lchunk = lane % CPR;
-  int64_t ga[IA], gw[IW];
-#pragma unroll
-  for (int i = 0; i < IA; ++i) {
-    const int row = (wave * IA + i) * RPI + lrow;
-    ga[i] = (int64_t)min(m0 + row, M - 1) * K + (lchunk ^ swz_rows<KS>(row)) * 16;
-  }
-#pragma unroll
-  for (int i = 0; i < IW; ++i) {
-    const int row = (wave * IW + i) * RPI + lrow;
-    gw[i] = (int64_t)min(n0 + row, N - 1) * K + (lchunk ^ swz_rows<KS>(row)) * 16;
-  }
-  // touch addressing: thread t covers tile rows t, t + NW*64, ... (A rows first, then W)
-  const uint8_t* tbase[TPL];
-#pragma unroll
-  for (int u = 0; u < TPL; ++u) {
-    const int trow = min((int)threadIdx.x + u * NW * 64, BM + BN - 1);
-    tbase[u] = trow < BM ? A + (int64_t)min(m0 + trow, M - 1) * K
-                         : W + (int64_t)min(n0 + trow - BM, N - 1) * K;
-  }
-  const int nk = K / KS;
-  auto touch = [&](int kt) {
-    if constexpr (TOUCH > 0) {
-      if (kt < nk) {
-#pragma unroll
-        for (int u = 0; u < TPL; ++u)
-          __builtin_amdgcn_global_load_lds((const void*)(tbase[u] + (int64_t)kt * KS),
-                                           (lds_void*)(lds + STAGES * SLOT + wave * 256), 4, 0, 0);
-      }
-    }
-  };
-  auto issue = [&](int slot, int kt) {
-    const int64_t koff = (int64_t)kt * KS;
-    uint8_t* base = lds + slot * SLOT;
-#pragma unroll
-    for (int i = 0; i < IA; ++i)
-      __builtin_amdgcn_global_load_lds((const void*)(A + ga[i] + koff),
-                                       (lds_void*)(base + (wave * IA + i) * 1024), 16, 0, 0);
-#pragma unroll
-    for (int i = 0; i < IW; ++i)
-      __builtin_amdgcn_global_load_lds((const void*)(W + gw[i] + koff),
-                                       (lds_void*)(base + A_BYTES + (wave * IW + i) * 1024), 16, 0,
-                                       0);
-  };
-
-  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
-  const int frow = lane & 31, g = lane >> 5;
-  const int fsw = swz_rows<KS>(frow);  // fragment rows differ from frow by multiples of 32
-  const int a_row0 = (wm * WTM + frow) * KS, w_row0 = A_BYTES + (wn * WTN + frow) * KS;
-
-  v16f acc[FN][FM];
-#pragma unroll
-  for (int i = 0; i < FN; ++i)
-#pragma unroll
-    for (int j = 0; j < FM; ++j) acc[i][j] = (v16f){};
-
-  auto compute = [&](int slot) {
-    const uint8_t* base = lds + slot * SLOT;
-#pragma unroll
-    for (int kk = 0; kk < KS / 64; ++kk) {
-      const int off0 = ((kk * 4 + 2 * g) ^ fsw) * 16, off1 = ((kk * 4 + 2 * g + 1) ^ fsw) * 16;
-      v8i fw[FN], fa[FM];
-#pragma unroll
-      for (int f = 0; f < FN; ++f) {
-        const uint8_t* r = base + w_row0 + f * 32 * KS;
-        const v4i lo = *(const v4i*)(r + off0);
-        const v4i hi = *(const v4i*)(r + off1);
-        fw[f] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-      }
-#pragma unroll
-      for (int f = 0; f < FM; ++f) {
-        const uint8_t* r = base + a_row0 + f * 32 * KS;
-        const v4i lo = *(const v4i*)(r + off0);
-        const v4i hi = *(const v4i*)(r + off1);
-        fa[f] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-      }
-#pragma unroll
-      for (int i = 0; i < FN; ++i)
-#pragma unroll
-        for (int j = 0; j < FM; ++j) acc[i][j] = mfma_32x32x64_fp8(fw[i], fa[j], acc[i][j]);
-    }
-  };
-
-#pragma unroll
-  for (int t = STAGES - 1; t < STAGES - 1 + TOUCH; ++t) touch(t);
-#pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s)
-    if (s < nk) {
-      issue(s, s);
-      touch(s + STAGES - 1 + TOUCH);
-    }
-  int slot = 0;
-  for (int kt = 0; kt < nk; ++kt) {
-    // stage kt has landed once at most the loads issued after it are in flight:
-    // its own step's touch plus (STAGES-2) full steps
-    if (kt + STAGES - 2 < nk) {
-      wait_vmcnt<(STAGES - 2) * PER_STEP + TLOADS>();
-    } else {
-      wait_vmcnt<0>();
-    }
-    block_barrier();  // stage kt visible to all waves; slot of stage kt-1 is free
-    if (kt + STAGES - 1 < nk) {
-      issue(slot == 0 ? STAGES - 1 : slot - 1, kt + STAGES - 1);
-      touch(kt + STAGES - 1 + TOUCH);
-    }
-    compute(slot);
-    slot = slot + 1 == STAGES ? 0 : slot + 1;
-  }
-
-  store_tile<kBf16, kGelu, FN, FM>(acc, m0 + wm * WTM, n0 + wn * WTN, frow, g, sa, sb, bias, C, M, N, ldc);
 }
 
 // Generic fallback for any M, N, K with K % 16 == 0: one wave computes a 32x32
@@ -525,191 +273,257 @@ __global__ __launch_bounds__(256) void fp8_gemm_generic(
   }
 }
 
-// Large-M kernel variant and L2 tile grouping (tuning switches while the
-// pipelined kernel is evaluated): JOY_GEMM_VARIANT, JOY_GEMM_GROUP_M.
-int gemm_variant() {
-  static const int v = [] {
-    const char* e = getenv("JOY_GEMM_VARIANT");
-    return e ? atoi(e) : 3;
-  }();
-  return v;
-}
-
-int gemm_group_m() {
-  static const int v = [] {
-    const char* e = getenv("JOY_GEMM_GROUP_M");
-    return e ? atoi(e) : 4;
-  }();
-  return v;
-}
-
-template <bool kBf16, bool kGelu, int BM, int BN, int WM_, int WN_, int ST, int KS, int TOUCH = 0>
-hipError_t launch_pipe(const GemmArgs& g, hipStream_t st) {
-  const int tiles_m = (g.M + BM - 1) / BM, tiles_n = (g.N + BN - 1) / BN;
-  hipLaunchKernelGGL((fp8_gemm_pipe<kBf16, kGelu, BM, BN, WM_, WN_, ST, KS, TOUCH>), dim3(tiles_m * tiles_n),
-                     dim3(WM_ * WN_ * 64), 0, st, (const uint8_t*)g.A, (const uint8_t*)g.W,
-                     g.scales_a, g.scales_b, (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N, g.K,
-                     g.ldc, tiles_m, tiles_n, gemm_group_m());
-  return hipGetLastError();
+// Instruction interleave of one main-loop iteration (N MFMAs, R fragment reads, L
+// DMAs) as sched_group_barrier groups emitted after MFMA number I: ceil(R/N) reads
+// and one DMA after each MFMA until both run out. (Spreading the DMAs over the whole
+// iteration, or reads first and DMAs last, measured the same on MI355X.)
+template <int I, int N, int R, int L>
+__device__ __forceinline__ void sched_pattern() {
+  if constexpr (I < N) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+    constexpr int RD = (R + N - 1) / N;
+    if constexpr (I * RD < R) __builtin_amdgcn_sched_group_barrier(0x100, RD, 0);  // LDS reads
+    if constexpr (I < L) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);        // one DMA
+    sched_pattern<I + 1, N, R, L>();
+  }
 }
 
 // ---------------------------------------------------------------------------
-// Ring kernel: 256x256 tile, K step 128 bytes (whole 128-byte lines per DMA
-// instruction), LDS used as a ring of five 32 KiB half-stages (the A half and the
-// W half of a K step), i.e. all 160 KiB. While step kt is computed, A(kt+1),
-// W(kt+1) and A(kt+2) are in flight: 1.5 steps of loads instead of 1 for a
-// two-slot double buffer. Half h of the sequence A0 W0 A1 W1 ... lives in slot h % 5.
+// Four-wave software-pipelined kernel: BM x BN tile (256x256 for the bulk of a
+// large GEMM; 128-row/column tiles for the last, partial round), one wave per
+// SIMD, each wave a (BM/2) x (BN/2) sub-tile of 32x32 MFMA tiles (up to 256 fp32
+// accumulators per lane, in AGPRs).
+//
+// LDS is a ring of S stages of one 64-byte K step ((BM + BN) rows x 64 B).
+// Iteration kt computes on fragments of step kt already in registers while it
+//   * reads the fragments of step kt+1 from LDS into the other register set, and
+//   * DMAs step kt+S into the slot of step kt (free: its fragments were read in
+//     iteration kt-1 and every wave passed this iteration's barrier),
+// with the three instruction streams interleaved one MFMA at a time. The loop body
+// is one basic block: past the last step the DMA re-fetches the last step (a slot
+// nobody reads again) and the extra fragment read is discarded, so every iteration
+// waits on the same constant vmcnt.
+//
+// Tile source. Bulk launch (sub_log2 < 0): block b takes position
+// xcd_position(b) of the grouped 256x256 tile order, positions [0, gridDim.x).
+// Tail launch (sub_log2 >= 0): block b takes sub-tile (b mod 2^sub_log2) of the
+// 256x256 tile at position tile_base + (b >> sub_log2).
 // ---------------------------------------------------------------------------
-template <bool kBf16, bool kGelu, int WAVES_M, int WAVES_N>
-__global__ __launch_bounds__(WAVES_M * WAVES_N * 64, 1) void fp8_gemm_ring(
+template <bool kBf16, bool kGelu, int BM, int BN, int S>
+__global__ __launch_bounds__(256, 1) void fp8_gemm_4w(
     const uint8_t* __restrict__ A, const uint8_t* __restrict__ W, const float* __restrict__ sa,
     const float* __restrict__ sb, const uint16_t* __restrict__ bias, uint16_t* __restrict__ C,
-    int M, int N, int K, int64_t ldc, int tiles_m, int tiles_n, int group_m) {
-  constexpr int BM = 256, BN = 256, KS = 128, HALF = 256 * KS;  // 32 KiB
-  constexpr int NW = WAVES_M * WAVES_N;
-  constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
+    int M, int N, int K, int64_t ldc, int tiles_m, int tiles_n, int group_m, int tile_base,
+    int sub_log2) {
+  constexpr int KS = 64, NW = 4;
+  constexpr int WTM = BM / 2, WTN = BN / 2;  // wave sub-tile
   constexpr int FM = WTM / 32, FN = WTN / 32;
-  constexpr int RPI = 8;                 // rows per DMA instruction (8 x 128 B)
-  constexpr int IH = 256 / RPI / NW;     // DMA instructions per wave per half
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[5 * HALF];
+  constexpr int RPI = 16;                    // rows per DMA instruction (16 x 64 B)
+  constexpr int IA = BM / RPI / NW, IW = BN / RPI / NW;
+  constexpr int A_BYTES = BM * KS, SLOT = (BM + BN) * KS;
+  constexpr int LOADS = IA + IW;
+  constexpr int NMFMA = FM * FN, NREAD = 2 * (FM + FN);
+  static_assert(IA * RPI * NW == BM && IW * RPI * NW == BN, "tile rows must split over waves");
+  static_assert((S - 2) * LOADS < 64, "vmcnt range");
+  constexpr int STAGE_BYTES = WTM * (WTN * 2 + 16);  // epilogue staging per wave
+  constexpr int LDS_BYTES = S * SLOT > NW * STAGE_BYTES ? S * SLOT : NW * STAGE_BYTES;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const TileCoord tc = map_tile(blockIdx.x, tiles_m, tiles_n, group_m);
-  const int m0 = tc.tm * BM, n0 = tc.tn * BN;
-
-  const int lrow = lane >> 3, lchunk = lane & 7;
-  int64_t ga[IH], gw[IH];
-#pragma unroll
-  for (int i = 0; i < IH; ++i) {
-    const int row = (wave * IH + i) * RPI + lrow;
-    const int c = (lchunk ^ swz_rows<KS>(row)) * 16;
-    ga[i] = (int64_t)min(m0 + row, M - 1) * K + c;
-    gw[i] = (int64_t)min(n0 + row, N - 1) * K + c;
+  int m0, n0;
+  if (sub_log2 < 0) {
+    const TileCoord tc = map_tile(blockIdx.x, gridDim.x, tiles_m, tiles_n, group_m, 0);
+    m0 = tc.tm * 256;
+    n0 = tc.tn * 256;
+  } else {
+    const TileCoord tc = map_tile(blockIdx.x >> sub_log2, -1, tiles_m, tiles_n, group_m, tile_base);
+    const int sub = blockIdx.x & ((1 << sub_log2) - 1);
+    constexpr int SUB_M = 256 / BM;
+    m0 = tc.tm * 256 + (sub % SUB_M) * BM;
+    n0 = tc.tn * 256 + (sub / SUB_M) * BN;
   }
-  auto issue_half = [&](const uint8_t* src, const int64_t (&off)[IH], int slot, int kt) {
-    const int64_t koff = (int64_t)kt * KS;
-    uint8_t* base = lds + slot * HALF;
+
+  // DMA: lane l of an instruction writes LDS row l/4, physical 16-byte chunk l%4,
+  // fetching logical chunk (l%4) ^ swz(row) of that row.
+  const int lrow = lane >> 2, lchunk = lane & 3;
+  const uint8_t* pa[IA];
+  const uint8_t* pw[IW];
 #pragma unroll
-    for (int i = 0; i < IH; ++i)
-      __builtin_amdgcn_global_load_lds((const void*)(src + off[i] + koff),
-                                       (lds_void*)(base + (wave * IH + i) * 1024), 16, 0, 0);
+  for (int i = 0; i < IA; ++i) {
+    const int row = (wave * IA + i) * RPI + lrow;
+    pa[i] = A + (int64_t)min(m0 + row, M - 1) * K + (lchunk ^ swz_rows<KS>(row)) * 16;
+  }
+#pragma unroll
+  for (int i = 0; i < IW; ++i) {
+    const int row = (wave * IW + i) * RPI + lrow;
+    pw[i] = W + (int64_t)min(n0 + row, N - 1) * K + (lchunk ^ swz_rows<KS>(row)) * 16;
+  }
+  const int nk = K / KS;
+  auto issue = [&](int slot, int kt) {
+    const int64_t koff = (int64_t)min(kt, nk - 1) * KS;
+    uint8_t* base = lds + slot * SLOT;
+#pragma unroll
+    for (int i = 0; i < IA; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(pa[i] + koff),
+                                       (lds_void*)(base + (wave * IA + i) * 1024), 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < IW; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(pw[i] + koff),
+                                       (lds_void*)(base + A_BYTES + (wave * IW + i) * 1024), 16, 0, 0);
   };
 
-  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  const int wm = wave >> 1, wn = wave & 1;
   const int frow = lane & 31, g = lane >> 5;
   const int fsw = swz_rows<KS>(frow);
-  const int a_row0 = (wm * WTM + frow) * KS, w_row0 = (wn * WTN + frow) * KS;
+  const int off0 = ((2 * g) ^ fsw) * 16, off1 = ((2 * g + 1) ^ fsw) * 16;
+  const int a_row0 = (wm * WTM + frow) * KS, w_row0 = A_BYTES + (wn * WTN + frow) * KS;
 
-  v16f acc[FN][FM];
+  v16f acc[FN][FM];  // [weight fragment][activation fragment]
 #pragma unroll
   for (int i = 0; i < FN; ++i)
 #pragma unroll
     for (int j = 0; j < FM; ++j) acc[i][j] = (v16f){};
 
-  auto compute = [&](int slot_a, int slot_w) {
-    const uint8_t* ba = lds + slot_a * HALF + a_row0;
-    const uint8_t* bw = lds + slot_w * HALF + w_row0;
+  v8i fw0[FN], fa0[FM], fw1[FN], fa1[FM];
+  auto read_frags = [&](int slot, v8i (&fw)[FN], v8i (&fa)[FM]) {
+    const uint8_t* base = lds + slot * SLOT;
 #pragma unroll
-    for (int kk = 0; kk < KS / 64; ++kk) {
-      const int off0 = ((kk * 4 + 2 * g) ^ fsw) * 16, off1 = ((kk * 4 + 2 * g + 1) ^ fsw) * 16;
-      v8i fw[FN], fa[FM];
+    for (int f = 0; f < FN; ++f) {
+      const uint8_t* r = base + w_row0 + f * 32 * KS;
+      const v4i lo = *(const v4i*)(r + off0);
+      const v4i hi = *(const v4i*)(r + off1);
+      fw[f] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
 #pragma unroll
-      for (int f = 0; f < FN; ++f) {
-        const v4i lo = *(const v4i*)(bw + f * 32 * KS + off0);
-        const v4i hi = *(const v4i*)(bw + f * 32 * KS + off1);
-        fw[f] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-      }
-#pragma unroll
-      for (int f = 0; f < FM; ++f) {
-        const v4i lo = *(const v4i*)(ba + f * 32 * KS + off0);
-        const v4i hi = *(const v4i*)(ba + f * 32 * KS + off1);
-        fa[f] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-      }
-#pragma unroll
-      for (int i = 0; i < FN; ++i)
-#pragma unroll
-        for (int j = 0; j < FM; ++j) acc[i][j] = mfma_32x32x64_fp8(fw[i], fa[j], acc[i][j]);
+    for (int f = 0; f < FM; ++f) {
+      const uint8_t* r = base + a_row0 + f * 32 * KS;
+      const v4i lo = *(const v4i*)(r + off0);
+      const v4i hi = *(const v4i*)(r + off1);
+      fa[f] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
     }
   };
+  auto mfmas = [&](const v8i (&fw)[FN], const v8i (&fa)[FM]) {
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j) acc[i][j] = mfma_32x32x64_fp8(fw[i], fa[j], acc[i][j]);
+  };
+  // One iteration: wait for step kt+1 (own DMAs) and for this wave's fragment reads,
+  // barrier, then DMA step kt+S into slot(kt), read step kt+1 from slot(kt+1), MFMA step kt.
+  auto iteration = [&](int kt, int slot, int next_slot, const v8i (&fw)[FN], const v8i (&fa)[FM],
+                       v8i (&nw)[FN], v8i (&na)[FM]) {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(((S - 2) * LOADS & 15) | ((((S - 2) * LOADS) >> 4) << 14) | 0x0070);
+    block_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    issue(slot, kt + S);
+    read_frags(next_slot, nw, na);
+    mfmas(fw, fa);
+    sched_pattern<0, NMFMA, NREAD, LOADS>();
+    __builtin_amdgcn_sched_barrier(0);
+  };
 
-  const int nk = K / KS;
-  // prologue: A0 W0 A1 -> slots 0 1 2
-  issue_half(A, ga, 0, 0);
-  issue_half(W, gw, 1, 0);
-  if (nk > 1) issue_half(A, ga, 2, 1);
-  int sa_slot = 0;  // slot of A(kt) = (2 kt) % 5; W(kt) is the next slot
-  for (int kt = 0; kt < nk; ++kt) {
-    // A(kt), W(kt) have landed once only A(kt+1) (issued after W(kt)) may be in flight
-    if (kt + 1 < nk) {
-      wait_vmcnt<IH>();
-    } else {
-      wait_vmcnt<0>();
-    }
-    block_barrier();  // step kt visible; the slots of step kt-1 are free
-    const int sw_slot = sa_slot == 4 ? 0 : sa_slot + 1;
-    // W(kt+1) goes to slot (2kt+3) % 5, A(kt+2) to (2kt+4) % 5: the slots of step kt-1
-    const int s3 = sa_slot + 3 >= 5 ? sa_slot - 2 : sa_slot + 3;
-    const int s4 = sa_slot + 4 >= 5 ? sa_slot - 1 : sa_slot + 4;
-    if (kt + 1 < nk) issue_half(W, gw, s3, kt + 1);
-    if (kt + 2 < nk) issue_half(A, ga, s4, kt + 2);
-    compute(sa_slot, sw_slot);
-    sa_slot = sa_slot + 2 >= 5 ? sa_slot - 3 : sa_slot + 2;
+  // prologue: steps 0..S-1 into slots 0..S-1, fragments of step 0
+#pragma unroll
+  for (int s = 0; s < S; ++s) issue(s, s);
+  wait_vmcnt<(S - 1) * LOADS>();
+  block_barrier();
+  read_frags(0, fw0, fa0);
+
+  int slot = 0;
+  int kt = 0;
+  for (; kt + 2 <= nk; kt += 2) {
+    const int s1 = slot + 1 == S ? 0 : slot + 1;
+    const int s2 = s1 + 1 == S ? 0 : s1 + 1;
+    iteration(kt, slot, s1, fw0, fa0, fw1, fa1);
+    iteration(kt + 1, s1, s2, fw1, fa1, fw0, fa0);
+    slot = s2;
   }
-  store_tile<kBf16, kGelu, FN, FM>(acc, m0 + wm * WTM, n0 + wn * WTN, frow, g, sa, sb, bias, C, M, N, ldc);
+  if (kt < nk) {  // odd step count: last step's fragments are in set 0
+    mfmas(fw0, fa0);
+  }
+  // epilogue operands; their latency overlaps the drain of the last DMAs and the barrier
+  ColOperands<FN> col;
+  load_col_operands<FN>(col, n0 + wn * WTN, g, N, sb, bias);
+  float sav[FM];
+#pragma unroll
+  for (int j = 0; j < FM; ++j) {
+    const int m = m0 + wm * WTM + j * 32 + frow;
+    sav[j] = m < M ? sa[m] : 0.0f;
+  }
+  // every wave's DMAs and fragment reads are done before LDS is reused for staging
+  wait_vmcnt<0>();
+  __builtin_amdgcn_s_waitcnt(0x0070);
+  block_barrier();
+  store_tile_lds<kBf16, kGelu, FN, FM>(acc, col, sav, lds + wave * STAGE_BYTES, m0 + wm * WTM,
+                                       n0 + wn * WTN, lane, C, M, N, ldc);
 }
 
-template <bool kBf16, bool kGelu, int WM_, int WN_>
-hipError_t launch_ring(const GemmArgs& g, hipStream_t st) {
+// Number of compute units of the current device (cached per device).
+int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
+// Full rounds of 256x256 tiles (one workgroup per CU), then the remaining tiles of
+// the last, partial round split into 4 (128x128) or 2 (256x128) sub-tiles so that
+// more CUs share that round. Both launches go to the same stream; the result does
+// not depend on the split (every output element sums its K products in the same order).
+template <bool kBf16, bool kGelu>
+hipError_t launch_4w(const GemmArgs& g, hipStream_t st) {
+  constexpr int S = 5;
   const int tiles_m = (g.M + 255) / 256, tiles_n = (g.N + 255) / 256;
-  hipLaunchKernelGGL((fp8_gemm_ring<kBf16, kGelu, WM_, WN_>), dim3(tiles_m * tiles_n),
-                     dim3(WM_ * WN_ * 64), 0, st, (const uint8_t*)g.A, (const uint8_t*)g.W,
-                     g.scales_a, g.scales_b, (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N, g.K,
-                     g.ldc, tiles_m, tiles_n, gemm_group_m());
+  const int T = tiles_m * tiles_n, P = device_cus();
+  int rem = T % P;
+  int sub_log2 = 0;
+  if (rem * 4 <= P) {
+    sub_log2 = 2;
+  } else if (rem * 2 <= P + P / 4) {
+    sub_log2 = 1;
+  } else {
+    rem = 0;  // the last round is nearly full: no split
+  }
+  const int bulk = T - rem;
+  if (bulk > 0) {
+    hipLaunchKernelGGL((fp8_gemm_4w<kBf16, kGelu, 256, 256, S>), dim3(bulk), dim3(256), 0, st,
+                       (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a, g.scales_b,
+                       (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tiles_m, tiles_n,
+                       kGroupM, 0, -1);
+  }
+  if (rem > 0) {
+    if (sub_log2 == 2) {
+      hipLaunchKernelGGL((fp8_gemm_4w<kBf16, kGelu, 128, 128, S>), dim3(rem << 2), dim3(256), 0, st,
+                         (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a, g.scales_b,
+                         (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tiles_m,
+                         tiles_n, kGroupM, bulk, 2);
+    } else {
+      hipLaunchKernelGGL((fp8_gemm_4w<kBf16, kGelu, 256, 128, S>), dim3(rem << 1), dim3(256), 0, st,
+                         (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a, g.scales_b,
+                         (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tiles_m,
+                         tiles_n, kGroupM, bulk, 1);
+    }
+  }
   return hipGetLastError();
 }
 
 template <bool kBf16, bool kGelu>
 hipError_t launch_gemm_t(const GemmArgs& g, hipStream_t st) {
-  const bool fast = (g.K % BK == 0) && (g.N % 8 == 0) && (g.ldc % 4 == 0) &&
-                    ((uintptr_t)g.C % 8 == 0) && ((uintptr_t)g.scales_b % 16 == 0) &&
-                    ((uintptr_t)g.A % 16 == 0) && ((uintptr_t)g.W % 16 == 0) &&
-                    ((uintptr_t)g.bias % 8 == 0) && !g.force_generic;
-  if (fast) {
-    switch (gemm_variant()) {
-      case 1:
-        return launch_pipe<kBf16, kGelu, 256, 256, 2, 2, 4, 64>(g, st);
-      case 2:
-        return launch_pipe<kBf16, kGelu, 256, 256, 2, 4, 4, 64>(g, st);
-      case 3:
-        return launch_pipe<kBf16, kGelu, 256, 256, 2, 4, 2, 128>(g, st);
-      case 4:
-        return launch_pipe<kBf16, kGelu, 256, 256, 2, 2, 2, 128>(g, st);
-      case 5:
-        return launch_pipe<kBf16, kGelu, 256, 128, 2, 2, 3, 128>(g, st);
-      case 6:
-        return launch_pipe<kBf16, kGelu, 128, 256, 2, 2, 3, 128>(g, st);
-      case 7:
-        return launch_pipe<kBf16, kGelu, 256, 256, 2, 4, 2, 128, 2>(g, st);
-      case 8:
-        return launch_pipe<kBf16, kGelu, 256, 256, 2, 4, 2, 128, 3>(g, st);
-      case 9:
-        return launch_pipe<kBf16, kGelu, 256, 256, 2, 2, 2, 128, 2>(g, st);
-      case 10:
-        return launch_ring<kBf16, kGelu, 2, 4>(g, st);
-      case 11:
-        return launch_ring<kBf16, kGelu, 2, 2>(g, st);
-      default:
-        break;
-    }
-    constexpr int BM = JOY_BM, BN = JOY_BN, WM_ = JOY_WM, WN_ = JOY_WN;
-    const int tiles_m = (g.M + BM - 1) / BM, tiles_n = (g.N + BN - 1) / BN;
-    hipLaunchKernelGGL((fp8_gemm_tiled<kBf16, kGelu, BM, BN, WM_, WN_>), dim3(tiles_m * tiles_n),
-                       dim3(WM_ * WN_ * 64), 0, st, (const uint8_t*)g.A, (const uint8_t*)g.W,
-                       g.scales_a, g.scales_b, (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N,
-                       g.K, g.ldc, tiles_m, tiles_n, 4);
-    return hipGetLastError();
-  }
+  // main kernel: 64-byte K steps, 16-byte operand rows and scale loads, 8-byte bias
+  // loads, 16-byte output row segments
+  const bool fast = !g.force_generic && g.K >= 64 && (g.K % 64 == 0) && (g.N % 8 == 0) &&
+                    (g.ldc % 8 == 0) && ((uintptr_t)g.C % 16 == 0) &&
+                    ((uintptr_t)g.scales_b % 16 == 0) && ((uintptr_t)g.A % 16 == 0) &&
+                    ((uintptr_t)g.W % 16 == 0) && ((uintptr_t)g.bias % 8 == 0);
+  if (fast) return launch_4w<kBf16, kGelu>(g, st);
   const int tiles_m = (g.M + 31) / 32, tiles_n = (g.N + 31) / 32;
   const int tiles = tiles_m * tiles_n;
   hipLaunchKernelGGL((fp8_gemm_generic<kBf16, kGelu>), dim3((tiles + 3) / 4), dim3(256), 0, st,

@@ -21,8 +21,6 @@
 // every load and store is a fully coalesced 128-bit access. The RMS reduction
 // runs over the D/8 lanes of a head with xor shuffles; RoPE pairs are adjacent
 // inside a lane, so rotation needs no cross-lane traffic.
-#include <stdlib.h>
-
 #include "joy_common.hpp"
 #include "joy_kernels.hpp"
 
@@ -153,36 +151,17 @@ __global__ __launch_bounds__(512) void qk_norm_rope_kernel(NormRopeArgs a) {
   }
 }
 
-// Tuning switches while the launch shape is evaluated: JOY_QKV_CFG = UPT*100 + NT*10 + waves/4.
-int qkv_cfg() {
-  static const int v = [] {
-    const char* e = getenv("JOY_QKV_CFG");
-    return e ? atoi(e) : 112;
-  }();
-  return v;
-}
-
-template <int D, int UPT, bool NT>
-hipError_t launch_norm_rope(const NormRopeArgs& a, hipStream_t st, int wpb) {
-  const int64_t units = a.n_tokens * a.num_heads;
-  constexpr int HPW = kWave / (D / 8);
-  const int64_t waves = (units + HPW * UPT - 1) / (HPW * UPT);
-  hipLaunchKernelGGL((qk_norm_rope_kernel<D, UPT, NT>), dim3((unsigned)((waves + wpb - 1) / wpb)),
-                     dim3(wpb * kWave), 0, st, a);
-  return hipGetLastError();
-}
-
+// Launch: one (token, head) group per wave (UPT = 1), non-temporal traffic, 8 waves
+// per workgroup -- the best of the shapes measured on MI355X for L = 10800, H = 40.
 template <int D>
 hipError_t launch_norm_rope_d(const NormRopeArgs& a, hipStream_t st) {
-  const int cfg = qkv_cfg();
-  const int wpb = (cfg % 10) == 2 ? 8 : 4;
-  const bool nt = (cfg / 10) % 10 == 1;
-  switch (cfg / 100) {
-    case 2:
-      return nt ? launch_norm_rope<D, 2, true>(a, st, wpb) : launch_norm_rope<D, 2, false>(a, st, wpb);
-    default:
-      return nt ? launch_norm_rope<D, 1, true>(a, st, wpb) : launch_norm_rope<D, 1, false>(a, st, wpb);
-  }
+  constexpr int UPT = 1, WPB = 8;
+  constexpr int HPW = kWave / (D / 8);
+  const int64_t units = a.n_tokens * a.num_heads;
+  const int64_t waves = (units + HPW * UPT - 1) / (HPW * UPT);
+  hipLaunchKernelGGL((qk_norm_rope_kernel<D, UPT, true>), dim3((unsigned)((waves + WPB - 1) / WPB)),
+                     dim3(WPB * kWave), 0, st, a);
+  return hipGetLastError();
 }
 
 }  // namespace

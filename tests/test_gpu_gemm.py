@@ -80,6 +80,23 @@ def test_exact_small_integers_bit_exact(M, N, K):
     assert np.array_equal(u16(gemm(qa, qw, sa, sw, None)), exp_nb)
 
 
+@pytest.mark.parametrize("M,N", [(4352, 4096), (5376, 4096)])
+def test_exact_full_rounds_plus_split_tail(M, N):
+    """More 256x256 tiles than CUs: full rounds run as 256x256 tiles and the last,
+    partial round as sub-tiles (on 256 CUs: 272 tiles -> 16 tiles in 4 sub-tiles each;
+    336 tiles -> 80 tiles in 2 sub-tiles each). Exact arithmetic fixes every bit."""
+    announce("gemm exact split tail", M, N)
+    K = 128
+    rng = np.random.default_rng(M + N)
+    qa = f32_to_e4m3fn(rng.integers(-8, 9, (M, K)).astype(np.float32))
+    qw = f32_to_e4m3fn(rng.integers(-8, 9, (N, K)).astype(np.float32))
+    sa = (2.0 ** rng.integers(-8, 2, M)).astype(np.float32)
+    sw = (2.0 ** rng.integers(-8, 2, N)).astype(np.float32)
+    bias = f32_to_bf16((rng.integers(-64, 64, N) / 16).astype(np.float32))
+    exp_bits, _ = og.scaled_mm(qa, qw, sa, sw, bias)
+    assert np.array_equal(u16(gemm(qa, qw, sa, sw, bias)), exp_bits)
+
+
 def test_cfg0_single_linear():
     announce("gemm cfg0 256x4096x4096")
     qa, sa, qw, sw, bias = quantized_problem(256, 4096, 4096, 0)
