@@ -102,6 +102,11 @@ def _time_eager(fn, steps: int):
     return start.elapsed_time(end) / 1e3 / steps
 
 
+def progress(msg: str) -> None:
+    """One line on stderr per finished section, so a long run shows it is alive."""
+    print(f"bench: {msg}", file=sys.stderr, flush=True)
+
+
 def load_traffic(name: str):
     """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
     calibrated on a copy kernel), committed as profiles/hbm_traffic.json."""
@@ -317,6 +322,7 @@ def main():
         rec["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                            "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": load_traffic("qkv_norm_rope"),
                            "algorithmic_bytes": b, "kernel": "qk_norm_rope_kernel<128>"}
+        progress(f"cfg1 qkv norm/rope {t * 1e6:.1f} us, {gbs:.0f} GB/s")
     if args.only in ("all", "gemm"):
         res, agg, ref_agg = bench_gemm(max(5, args.steps // 5), max(2, args.warmup // 2))
         best = max(res, key=lambda r: r["tflops"])
@@ -326,12 +332,15 @@ def main():
                                          "unit": "TFLOP/s", "frac": round(agg / PEAK_FP8_TFLOPS, 4),
                                          "traffic": load_traffic("fp8_gemm_qkv"),
                                          "best_shape": best["shape"]}}
+        progress(f"cfg2 GEMMs {agg:.0f} TFLOP/s aggregate")
         if "value" not in rec:
             rec.update({"value": round(agg, 1), "unit": "TFLOP/s", "ms_per_step": sum(r["ms"] for r in res)})
     if args.only in ("all", "small"):
         rec["gemm_cfg3_small_m"] = bench_small_m(args.steps, args.warmup)
+        progress("cfg3 small-M GEMMs done")
     if args.only in ("all", "quant"):
         rec["act_quant"] = bench_quant(args.steps, args.warmup)
+        progress("act quant done")
     if args.only == "copy":
         rec["copy"] = bench_copy(args.steps, args.warmup)
     if not args.no_cpu:
