@@ -226,6 +226,41 @@ def bench_quant(steps, warmup):
     return out
 
 
+def bench_pack(steps, warmup):
+    """Cache read side at cfg-4 geometry: fused_cached_kv_pack over two KV-ring
+    slots (2 x 10800 tokens, fp32 full-width tables) and fused_joint_qkv_pack of
+    3 cached chunks + 10800 video tokens (strided views of the QKV GEMM row) +
+    512 condition tokens (two-rounding RMSNorm)."""
+    import torch
+    import joyomni_ops as jo
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(3)
+    L, T, C = L_TOK, 512, 3 * L_TOK
+    ring_k = torch.randn(RING_SLOTS, L, HEADS, HEAD_DIM, generator=g).to(torch.bfloat16).to(dev)
+    ring_v = torch.randn(RING_SLOTS, L, HEADS, HEAD_DIM, generator=g).to(torch.bfloat16).to(dev)
+    cos = torch.rand(2 * L, HEAD_DIM, generator=g).to(dev)
+    sin = torch.rand(2 * L, HEAD_DIM, generator=g).to(dev)
+    out = []
+    t = time_launches(lambda: jo.fused_cached_kv_pack(ring_k[2][None], ring_v[2][None], ring_k[0][None],
+                                                      ring_v[0][None], cos, sin), steps, warmup)
+    b = 2 * (2 * L) * E * 2 + 2 * (2 * L) * HEAD_DIM * 4 + 2 * (2 * L) * E * 2
+    out.append({"op": "fused_cached_kv_pack", "tokens": 2 * L, "us": t * 1e6, "gbs": b / t / 1e9,
+                "frac_hbm_peak": b / t / 1e9 / PEAK_HBM_GBS, "algorithmic_bytes": b})
+    img = torch.randn(L, 3 * E, generator=g).to(torch.bfloat16).to(dev).view(1, L, 3, HEADS, HEAD_DIM)
+    txt = torch.randn(T, 3 * E, generator=g).to(torch.bfloat16).to(dev).view(1, T, 3, HEADS, HEAD_DIM)
+    w = torch.ones(HEAD_DIM, dtype=torch.bfloat16, device=dev)
+    ck = ring_k[:3].reshape(1, C, HEADS, HEAD_DIM)
+    cv = ring_v[:3].reshape(1, C, HEADS, HEAD_DIM)
+    t = time_launches(lambda: jo.fused_joint_qkv_pack(img[:, :, 0], img[:, :, 1], img[:, :, 2], txt[:, :, 0],
+                                                      txt[:, :, 1], txt[:, :, 2], ck, cv, w, w, 1e-6),
+                      steps, warmup)
+    b = (3 * (L + T) + 2 * C) * E * 2 + 2 * HEAD_DIM * 2 + ((L + T) + 2 * (C + L + T)) * E * 2
+    out.append({"op": "fused_joint_qkv_pack", "tokens": {"cache": C, "video": L, "condition": T},
+                "us": t * 1e6, "gbs": b / t / 1e9, "frac_hbm_peak": b / t / 1e9 / PEAK_HBM_GBS,
+                "algorithmic_bytes": b})
+    return out
+
+
 def bench_copy(steps, warmup):
     """Plain 1 GiB device-to-device copy: the calibration kernel for the
     FETCH_SIZE / WRITE_SIZE counters (known 1 GiB read + 1 GiB write)."""
@@ -294,7 +329,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time plain launches (no HIP graph)")
-    ap.add_argument("--only", default="all", choices=["all", "qkv", "gemm", "small", "quant", "copy"])
+    ap.add_argument("--only", default="all", choices=["all", "qkv", "gemm", "small", "quant", "pack", "copy"])
     args = ap.parse_args()
     global EAGER
     EAGER = args.eager
@@ -341,6 +376,9 @@ def main():
     if args.only in ("all", "quant"):
         rec["act_quant"] = bench_quant(args.steps, args.warmup)
         progress("act quant done")
+    if args.only in ("all", "pack"):
+        rec["kv_pack"] = bench_pack(args.steps, args.warmup)
+        progress("cache read-side packs done")
     if args.only == "copy":
         rec["copy"] = bench_copy(args.steps, args.warmup)
     if not args.no_cpu:

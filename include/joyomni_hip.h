@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define JOY_ABI_VERSION 1
+#define JOY_ABI_VERSION 2
 
 #if defined(__GNUC__) || defined(__clang__)
 #define JOY_API __attribute__((visibility("default")))
@@ -127,6 +127,63 @@ JOY_API joy_status joy_fused_qkv_norm_rope_cache(const void *qkv, int64_t qkv_ro
                                          void *cache_k, void *cache_v, int64_t num_slots,
                                          int64_t slot_capacity, int64_t slot, int64_t slot_offset,
                                          void *stream);
+
+/*
+ * A bf16 [len, num_heads, head_dim] view with a dense last dimension: element
+ * (t, h, d) is at ((const uint16_t *)ptr)[t * stride_token + h * stride_head + d]
+ * (strides in elements). This is what a reference [1, L, H, D] tensor with
+ * stride(3) == 1 passes (fused_joint_qkv_pack.cu:222-229), e.g. the q/k/v
+ * slices of the QKV projection output.
+ */
+typedef struct {
+  const void *ptr;
+  int64_t len;
+  int64_t stride_token;
+  int64_t stride_head;
+} joy_bf16_view;
+
+/*
+ * Joint-attention Q/K/V pack with text Q/K RMSNorm.
+ * Replaces: fused_joint_qkv_pack(Tensor img_q, Tensor img_k, Tensor img_v, Tensor txt_q,
+ *           Tensor txt_k, Tensor txt_v, Tensor? cached_k, Tensor? cached_v,
+ *           Tensor txt_q_weight, Tensor txt_k_weight, float eps) -> (Tensor, Tensor, Tensor)
+ *   schema joyomni_ops/csrc/pybind.cpp:56-59, impl joyomni_ops/csrc/fused_joint_qkv_pack.cu:237-342
+ *   (kernel :81-164).
+ *   out_q = [img_q | rms(txt_q)]            dense [img_len + txt_len, H, D]
+ *   out_k = [cached_k | img_k | rms(txt_k)]  dense [cache_len + img_len + txt_len, H, D]
+ *   out_v = [cached_v | img_v | txt_v]       same shape as out_k
+ *   rms(x) = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w)  (two roundings, :58-79)
+ * cached_k, cached_v: NULL (or ptr NULL) for no cache; both or neither.
+ * Outputs are caller-allocated (the reference allocates them, :290-293).
+ * head_dim must be 128 (reference rule); img_len, txt_len, num_heads > 0.
+ */
+JOY_API joy_status joy_fused_joint_qkv_pack(const joy_bf16_view *img_q, const joy_bf16_view *img_k,
+                                    const joy_bf16_view *img_v, const joy_bf16_view *txt_q,
+                                    const joy_bf16_view *txt_k, const joy_bf16_view *txt_v,
+                                    const joy_bf16_view *cached_k, const joy_bf16_view *cached_v,
+                                    const void *txt_q_weight, const void *txt_k_weight, float eps,
+                                    int64_t num_heads, int64_t head_dim, void *out_q, void *out_k,
+                                    void *out_v, void *stream);
+
+/*
+ * Rotate and pack one or two pre-RoPE cached K segments with their V.
+ * Replaces: fused_cached_kv_pack(Tensor key0, Tensor value0, Tensor? key1, Tensor? value1,
+ *           Tensor cos, Tensor sin) -> (Tensor, Tensor)
+ *   schema joyomni_ops/csrc/pybind.cpp:60-62, impl joyomni_ops/csrc/fused_joint_qkv_pack.cu:344-415
+ *   (kernel :166-220).
+ *   out_k[t] = rotate(key[t]) with pair (2i, 2i+1):
+ *     o_2i = k_2i * c - k_2i+1 * s ; o_2i+1 = k_2i * s + k_2i+1 * c, c, s = cos/sin[t * D + 2i]
+ *   out_v[t] = value[t]; t runs over key0's tokens, then key1's.
+ * cos, sin: fp32 [len0 + len1, head_dim] (full width, repeat_interleave layout).
+ * key1/value1: NULL (or ptr NULL) for one segment; both or neither.
+ * Outputs: caller-allocated dense [len0 + len1, H, D]. A ring slot (rows of
+ * cache_k[slot]) is a valid key view, so this reads the KV ring directly.
+ * head_dim must be 128; len0, num_heads > 0; len1 > 0 when present.
+ */
+JOY_API joy_status joy_fused_cached_kv_pack(const joy_bf16_view *key0, const joy_bf16_view *value0,
+                                    const joy_bf16_view *key1, const joy_bf16_view *value1,
+                                    const float *cos, const float *sin, int64_t num_heads,
+                                    int64_t head_dim, void *out_k, void *out_v, void *stream);
 
 #ifdef __cplusplus
 }

@@ -209,3 +209,114 @@ joy_status joy_fused_qkv_norm_rope_cache(const void* qkv, int64_t qkv_row_stride
 }
 
 }  // extern "C"
+
+namespace {
+
+bool present(const joy_bf16_view* v) { return v != nullptr && v->ptr != nullptr; }
+
+joy::RowView row_view(const joy_bf16_view* v) {
+  joy::RowView r;
+  r.ptr = present(v) ? (const uint16_t*)v->ptr : nullptr;
+  r.stride_token = present(v) ? v->stride_token : 0;
+  r.stride_head = present(v) ? v->stride_head : 0;
+  return r;
+}
+
+// Largest row count of the pack kernels' grid (16 rows per workgroup).
+constexpr int64_t kMaxPackRows = 0xffffffffLL * 16;
+
+}  // namespace
+
+extern "C" {
+
+joy_status joy_fused_joint_qkv_pack(const joy_bf16_view* img_q, const joy_bf16_view* img_k,
+                                    const joy_bf16_view* img_v, const joy_bf16_view* txt_q,
+                                    const joy_bf16_view* txt_k, const joy_bf16_view* txt_v,
+                                    const joy_bf16_view* cached_k, const joy_bf16_view* cached_v,
+                                    const void* txt_q_weight, const void* txt_k_weight, float eps,
+                                    int64_t num_heads, int64_t head_dim, void* out_q, void* out_k,
+                                    void* out_v, void* stream) {
+  // checks of fused_joint_qkv_pack.cu:246-284
+  if (!present(img_q) || !present(img_k) || !present(img_v) || !present(txt_q) || !present(txt_k) ||
+      !present(txt_v))
+    return fail(JOY_ERR_INVALID_ARGUMENT, "img/txt q, k, v must be non-null");
+  if (head_dim != 128) return fail(JOY_ERR_INVALID_ARGUMENT, "fused_joint_qkv_pack requires head_dim=128");
+  const int64_t img_len = img_q->len;
+  if (img_len <= 0 || num_heads <= 0)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "image length and heads must be positive");
+  if (img_k->len != img_len || img_v->len != img_len)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "image Q/K/V lengths must match");
+  const int64_t txt_len = txt_q->len;
+  if (txt_len <= 0 || txt_k->len != txt_len || txt_v->len != txt_len)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "text Q/K/V lengths must match and be positive");
+  if (!txt_q_weight || !txt_k_weight)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "txt_q_weight and txt_k_weight must be non-null");
+  if (present(cached_k) != present(cached_v))
+    return fail(JOY_ERR_INVALID_ARGUMENT,
+                "cached_k and cached_v must either both be present or both be absent");
+  const int64_t cache_len = present(cached_k) ? cached_k->len : 0;
+  if (cache_len < 0 || (present(cached_v) && cached_v->len != cache_len))
+    return fail(JOY_ERR_INVALID_ARGUMENT, "cached K/V lengths must match");
+  if (!out_q || !out_k || !out_v) return fail(JOY_ERR_INVALID_ARGUMENT, "out_q, out_k and out_v must be non-null");
+  if (num_heads > 0x7fffffffLL) return fail(JOY_ERR_UNSUPPORTED, "num_heads too large");
+  if ((img_len + txt_len) * num_heads + 2 * (cache_len + img_len + txt_len) * num_heads > kMaxPackRows)
+    return fail(JOY_ERR_UNSUPPORTED, "too many rows for one launch");
+  joy::JointPackArgs a;
+  a.img_q = row_view(img_q);
+  a.img_k = row_view(img_k);
+  a.img_v = row_view(img_v);
+  a.txt_q = row_view(txt_q);
+  a.txt_k = row_view(txt_k);
+  a.txt_v = row_view(txt_v);
+  a.cache_k = row_view(cached_k);
+  a.cache_v = row_view(cached_v);
+  a.txt_q_weight = (const uint16_t*)txt_q_weight;
+  a.txt_k_weight = (const uint16_t*)txt_k_weight;
+  a.out_q = (uint16_t*)out_q;
+  a.out_k = (uint16_t*)out_k;
+  a.out_v = (uint16_t*)out_v;
+  a.img_len = img_len;
+  a.txt_len = txt_len;
+  a.cache_len = cache_len;
+  a.heads = (int)num_heads;
+  a.eps = eps;
+  return hip_status(joy::launch_joint_qkv_pack(a, (hipStream_t)stream), "fused_joint_qkv_pack launch");
+}
+
+joy_status joy_fused_cached_kv_pack(const joy_bf16_view* key0, const joy_bf16_view* value0,
+                                    const joy_bf16_view* key1, const joy_bf16_view* value1,
+                                    const float* cos, const float* sin, int64_t num_heads,
+                                    int64_t head_dim, void* out_k, void* out_v, void* stream) {
+  // checks of fused_joint_qkv_pack.cu:351-381
+  if (!present(key0) || !present(value0))
+    return fail(JOY_ERR_INVALID_ARGUMENT, "key0 and value0 must be non-null");
+  if (head_dim != 128) return fail(JOY_ERR_INVALID_ARGUMENT, "fused_cached_kv_pack requires head_dim=128");
+  const int64_t len0 = key0->len;
+  if (len0 <= 0 || num_heads <= 0) return fail(JOY_ERR_INVALID_ARGUMENT, "cache length and heads must be positive");
+  if (value0->len != len0) return fail(JOY_ERR_INVALID_ARGUMENT, "key0/value0 lengths must match");
+  if (present(key1) != present(value1))
+    return fail(JOY_ERR_INVALID_ARGUMENT, "key1 and value1 must either both be present or both be absent");
+  const int64_t len1 = present(key1) ? key1->len : 0;
+  if (present(key1) && (len1 <= 0 || value1->len != len1))
+    return fail(JOY_ERR_INVALID_ARGUMENT, "key1/value1 lengths must match and be positive");
+  if (!cos || !sin) return fail(JOY_ERR_INVALID_ARGUMENT, "cos and sin must be non-null");
+  if (!out_k || !out_v) return fail(JOY_ERR_INVALID_ARGUMENT, "out_k and out_v must be non-null");
+  if (num_heads > 0x7fffffffLL) return fail(JOY_ERR_UNSUPPORTED, "num_heads too large");
+  if (2 * (len0 + len1) * num_heads > kMaxPackRows)
+    return fail(JOY_ERR_UNSUPPORTED, "too many rows for one launch");
+  joy::CachedPackArgs a;
+  a.key0 = row_view(key0);
+  a.value0 = row_view(value0);
+  a.key1 = row_view(key1);
+  a.value1 = row_view(value1);
+  a.cos = cos;
+  a.sin = sin;
+  a.out_k = (uint16_t*)out_k;
+  a.out_v = (uint16_t*)out_v;
+  a.len0 = len0;
+  a.len1 = len1;
+  a.heads = (int)num_heads;
+  return hip_status(joy::launch_cached_kv_pack(a, (hipStream_t)stream), "fused_cached_kv_pack launch");
+}
+
+}  // extern "C"

@@ -44,9 +44,42 @@ struct GemmArgs {
   bool force_generic;
 };
 
+// bf16 [len, H, D] view: element (t, h, d) at ptr[t * stride_token + h * stride_head + d].
+struct RowView {
+  const uint16_t* ptr;  // null = absent segment
+  int64_t stride_token;
+  int64_t stride_head;
+};
+
+// fused_joint_qkv_pack: outputs are dense [rows, 128].
+struct JointPackArgs {
+  RowView img_q, img_k, img_v, txt_q, txt_k, txt_v, cache_k, cache_v;
+  const uint16_t* txt_q_weight;
+  const uint16_t* txt_k_weight;
+  uint16_t* out_q;
+  uint16_t* out_k;
+  uint16_t* out_v;
+  int64_t img_len, txt_len, cache_len;
+  int heads;
+  float eps;
+};
+
+// fused_cached_kv_pack: cos/sin fp32 [len0 + len1, 128]; outputs dense [rows, 128].
+struct CachedPackArgs {
+  RowView key0, value0, key1, value1;
+  const float* cos;
+  const float* sin;
+  uint16_t* out_k;
+  uint16_t* out_v;
+  int64_t len0, len1;
+  int heads;
+};
+
 hipError_t launch_per_token_quant(const void* in, bool in_fp16, void* q, float* s, int64_t M,
                                   int64_t K, bool divide, hipStream_t st);
 hipError_t launch_qk_norm_rope(const NormRopeArgs& a, int head_dim, hipStream_t st);
 hipError_t launch_fp8_gemm(const GemmArgs& g, hipStream_t st);
+hipError_t launch_joint_qkv_pack(const JointPackArgs& a, hipStream_t st);
+hipError_t launch_cached_kv_pack(const CachedPackArgs& a, hipStream_t st);
 
 }  // namespace joy

@@ -6,18 +6,19 @@ reference's ``joyomni_ops/joyomni_ops/__init__.py`` (schemas from
 ``from joyomni_ops import ...`` keep working for ``deploy/xvideo``.
 
 The quantised hot path -- ``sgl_per_token_quant_fp8``, ``fp8_scaled_mm``,
-``fused_qk_norm_rope_3d_paired`` and the new ``fused_qkv_norm_rope_cache`` --
-runs in hand-written gfx950 kernels of ``libjoyomni_hip.so`` reached through
-its C ABI (``include/joyomni_hip.h``). Importing fails when that library is
-missing, exactly like the reference (``__init__.py:15-19``); nothing falls back.
+``fused_qk_norm_rope_3d_paired``, the new ``fused_qkv_norm_rope_cache`` and the
+cache read side ``fused_joint_qkv_pack`` / ``fused_cached_kv_pack`` -- runs in
+hand-written gfx950 kernels of ``libjoyomni_hip.so`` reached through its C ABI
+(``include/joyomni_hip.h``). Importing fails when that library is missing,
+exactly like the reference (``__init__.py:15-19``); nothing falls back.
 
-Ops outside the quantised path (``fused_joint_qkv_pack``,
-``fused_cached_kv_pack``, ``fused_norm_scale_shift``, ``rmsnorm``) keep their
-reference schemas and are composed from torch device ops, so the reference's
-imports (``sgl_fused_ops.py:27-33``) still resolve.
+The two ops outside the quantised path (``fused_norm_scale_shift``,
+``rmsnorm``) keep their reference schemas and are composed from torch device
+ops, so the reference's imports (``sgl_fused_ops.py:27-33``) still resolve.
 """
 from __future__ import annotations
 
+import ctypes
 from typing import Optional
 
 import torch
@@ -283,44 +284,109 @@ def _fused_qkv_norm_rope_cache_cuda(qkv, num_heads, eps, q_weight, k_weight, cos
 
 
 # --------------------------------------------------------------------------
-# ops outside the quantised path: torch device compositions of the reference
-# semantics (sgl_fused_ops.py:202-209,257-265; fused_joint_qkv_pack.cu:58-79,210-219;
-# fused_norm_scale_shift.cu; rmsnorm.cu)
+# cache read side: joint Q/K/V pack and cached-K rotation (HIP kernels)
 # --------------------------------------------------------------------------
-def _rms_two_round(x, w, eps):
-    xf = x.float()
-    n = (xf * torch.rsqrt(xf.square().mean(-1, keepdim=True) + eps)).to(torch.bfloat16)
-    return n * w.to(torch.bfloat16)
+def _check_qkv_tensor(t, name, batch, heads, head_dim):
+    # check_qkv_tensor of fused_joint_qkv_pack.cu:222-229
+    _check(t.is_cuda, f"{name} must be a CUDA tensor")
+    _check(t.dtype == torch.bfloat16, f"{name} must be bfloat16")
+    _check(t.dim() == 4, f"{name} must be [B,L,H,D]")
+    _check(t.size(0) == batch and t.size(2) == heads and t.size(3) == head_dim,
+           f"{name} has incompatible shape {list(t.shape)}")
+    _check(t.stride(3) == 1, f"{name} last dimension must be contiguous")
+
+
+def _view(t: Optional[torch.Tensor]):
+    """joy_bf16_view of a [1, L, H, D] tensor (None -> NULL)."""
+    if t is None:
+        return None
+    return _lib.Bf16View(t.data_ptr(), t.size(1), t.stride(1), t.stride(2))
+
+
+def _vref(v):
+    return None if v is None else ctypes.byref(v)
 
 
 @torch.library.impl(_lib_def, "fused_joint_qkv_pack", "CUDA")
 def _fused_joint_qkv_pack_cuda(img_q, img_k, img_v, txt_q, txt_k, txt_v, cached_k, cached_v,
                                txt_q_weight, txt_k_weight, eps):
-    if (cached_k is None) != (cached_v is None):
-        raise RuntimeError("cached_k and cached_v must be provided together")
-    q = torch.cat((img_q, _rms_two_round(txt_q, txt_q_weight, eps)), dim=1)
-    k = torch.cat((img_k, _rms_two_round(txt_k, txt_k_weight, eps)), dim=1)
-    v = torch.cat((img_v, txt_v), dim=1)
+    # checks of fused_joint_qkv_pack.cu:244-284
+    _check(img_q.dim() == 4, "img_q must be [B,L,H,D]")
+    batch, img_len, heads, head_dim = img_q.shape
+    _check(batch == 1, "fused_joint_qkv_pack fast path requires batch=1")
+    _check(head_dim == 128, "fused_joint_qkv_pack requires head_dim=128")
+    _check(img_len > 0 and heads > 0, "image length and heads must be positive")
+    for name, t in (("img_q", img_q), ("img_k", img_k), ("img_v", img_v)):
+        _check_qkv_tensor(t, name, batch, heads, head_dim)
+    _check(img_k.size(1) == img_len and img_v.size(1) == img_len, "image Q/K/V lengths must match")
+    txt_len = txt_q.size(1) if txt_q.dim() == 4 else 0
+    for name, t in (("txt_q", txt_q), ("txt_k", txt_k), ("txt_v", txt_v)):
+        _check_qkv_tensor(t, name, batch, heads, head_dim)
+    _check(txt_len > 0 and txt_k.size(1) == txt_len and txt_v.size(1) == txt_len,
+           "text Q/K/V lengths must match and be positive")
+    for name, t in (("txt_q_weight", txt_q_weight), ("txt_k_weight", txt_k_weight)):
+        _check_input(t, name, torch.bfloat16)
+    _check(txt_q_weight.dim() == 1 and txt_q_weight.numel() == head_dim, "txt_q_weight must be [head_dim]")
+    _check(txt_k_weight.dim() == 1 and txt_k_weight.numel() == head_dim, "txt_k_weight must be [head_dim]")
+    _check((cached_k is None) == (cached_v is None),
+           "cached_k and cached_v must either both be present or both be absent")
+    cache_len = 0
     if cached_k is not None:
-        k = torch.cat((cached_k, k), dim=1)
-        v = torch.cat((cached_v, v), dim=1)
-    return q.contiguous(), k.contiguous(), v.contiguous()
+        _check_qkv_tensor(cached_k, "cached_k", batch, heads, head_dim)
+        _check_qkv_tensor(cached_v, "cached_v", batch, heads, head_dim)
+        cache_len = cached_k.size(1)
+        _check(cached_v.size(1) == cache_len, "cached K/V lengths must match")
+    out_q = img_q.new_empty((batch, img_len + txt_len, heads, head_dim))
+    out_k = img_q.new_empty((batch, cache_len + img_len + txt_len, heads, head_dim))
+    out_v = torch.empty_like(out_k)
+    views = [_view(t) for t in (img_q, img_k, img_v, txt_q, txt_k, txt_v, cached_k, cached_v)]
+    with torch.cuda.device(img_q.device):
+        st = _LIB.joy_fused_joint_qkv_pack(
+            *[_vref(v) for v in views], _ptr(txt_q_weight), _ptr(txt_k_weight), float(eps), heads,
+            head_dim, _ptr(out_q), _ptr(out_k), _ptr(out_v), _stream(img_q))
+    _lib.check(_LIB, st)
+    return out_q, out_k, out_v
 
 
 @torch.library.impl(_lib_def, "fused_cached_kv_pack", "CUDA")
 def _fused_cached_kv_pack_cuda(key0, value0, key1, value1, cos, sin):
-    keys = [key0] + ([key1] if key1 is not None else [])
-    vals = [value0] + ([value1] if value1 is not None else [])
-    k = torch.cat(keys, dim=1).float()
-    B, L, H, D = k.shape
-    pairs = k.reshape(B, L, H, D // 2, 2)
-    rot = torch.stack((-pairs[..., 1], pairs[..., 0]), dim=-1).flatten(-2)
-    c = cos.reshape(1, L, 1, D).float()
-    s = sin.reshape(1, L, 1, D).float()
-    out_k = (k * c + rot * s).to(key0.dtype)
-    return out_k, torch.cat(vals, dim=1).contiguous()
+    # checks of fused_joint_qkv_pack.cu:351-381
+    _check(key0.dim() == 4, "key0 must be [B,L,H,D]")
+    batch, len0, heads, head_dim = key0.shape
+    _check(batch == 1, "fused_cached_kv_pack requires batch=1")
+    _check(head_dim == 128, "fused_cached_kv_pack requires head_dim=128")
+    _check(len0 > 0 and heads > 0, "cache length and heads must be positive")
+    _check_qkv_tensor(key0, "key0", batch, heads, head_dim)
+    _check_qkv_tensor(value0, "value0", batch, heads, head_dim)
+    _check(value0.size(1) == len0, "key0/value0 lengths must match")
+    _check((key1 is None) == (value1 is None),
+           "key1 and value1 must either both be present or both be absent")
+    len1 = 0
+    if key1 is not None:
+        _check_qkv_tensor(key1, "key1", batch, heads, head_dim)
+        _check_qkv_tensor(value1, "value1", batch, heads, head_dim)
+        len1 = key1.size(1)
+        _check(len1 > 0 and value1.size(1) == len1, "key1/value1 lengths must match and be positive")
+    _check_input(cos, "cos", torch.float32)
+    _check_input(sin, "sin", torch.float32)
+    _check(cos.shape == sin.shape, "cos/sin shapes must match")
+    _check(cos.numel() == (len0 + len1) * head_dim,
+           f"cos/sin must contain [total_cache_len, head_dim], got {list(cos.shape)}")
+    out_k = key0.new_empty((batch, len0 + len1, heads, head_dim))
+    out_v = torch.empty_like(out_k)
+    views = [_view(t) for t in (key0, value0, key1, value1)]
+    with torch.cuda.device(key0.device):
+        st = _LIB.joy_fused_cached_kv_pack(
+            *[_vref(v) for v in views], _ptr(cos), _ptr(sin), heads, head_dim, _ptr(out_k), _ptr(out_v),
+            _stream(key0))
+    _lib.check(_LIB, st)
+    return out_k, out_v
 
 
+# --------------------------------------------------------------------------
+# ops outside the quantised path: torch device compositions of the reference
+# semantics (fused_norm_scale_shift.cu:97-182, rmsnorm.cu:60-84)
+# --------------------------------------------------------------------------
 @torch.library.impl(_lib_def, "fused_norm_scale_shift", "CUDA")
 def _fused_norm_scale_shift_cuda(x, gamma_opt, beta_opt, scale, shift, norm_type, eps):
     xf = x.float()

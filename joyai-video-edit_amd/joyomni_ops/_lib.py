@@ -30,6 +30,15 @@ _i64 = ctypes.c_int64
 _int = ctypes.c_int
 _f32 = ctypes.c_float
 
+
+class Bf16View(ctypes.Structure):
+    """joy_bf16_view: bf16 [len, H, D] view, element (t, h, d) at ptr[t*stride_token + h*stride_head + d]."""
+    _fields_ = [("ptr", ctypes.c_void_p), ("len", ctypes.c_int64), ("stride_token", ctypes.c_int64),
+                ("stride_head", ctypes.c_int64)]
+
+
+_view = ctypes.POINTER(Bf16View)
+
 # name -> (restype, argtypes); mirrors include/joyomni_hip.h one to one.
 SIGNATURES = {
     "joy_abi_version": (_int, []),
@@ -41,9 +50,14 @@ SIGNATURES = {
     "joy_fused_qkv_norm_rope_cache": (
         _int, [_vp, _i64, _i64, _i64, _i64, _f32, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64,
                _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
+    "joy_fused_joint_qkv_pack": (
+        _int, [_view, _view, _view, _view, _view, _view, _view, _view, _vp, _vp, _f32, _i64, _i64,
+               _vp, _vp, _vp, _vp]),
+    "joy_fused_cached_kv_pack": (
+        _int, [_view, _view, _view, _view, _vp, _vp, _i64, _i64, _vp, _vp, _vp]),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class JoyError(RuntimeError):

@@ -14,6 +14,9 @@ paths this repository implements on MI355X:
   (``joyomni_ops/csrc/fused_qknorm_rope_3d_kernel.cu:68-105``) and the fused
   QKV split / KV-ring write semantics (``deploy/xvideo/models/dit/dit.py:409-451``,
   ``dit.py:867-882``).
+* ``oracle.kvpack``  -- joint-attention Q/K/V pack with the two-rounding text
+  RMSNorm and the rotation of pre-RoPE cached K
+  (``joyomni_ops/csrc/fused_joint_qkv_pack.cu:58-220``).
 * ``oracle.rope``    -- 3-D (t,h,w) RoPE tables (``deploy/xvideo/models/dit/rope.py:31-52``,
   ``dit.py:896-934``, ``sgl_fused_ops.py:94-119``).
 * ``oracle.torch_path`` -- the reference's own CPU torch code path, restated,

@@ -95,3 +95,42 @@ def test_single_hip_runtime_in_process():
     maps = open("/proc/self/maps").read().splitlines()
     hip = {line.split()[-1] for line in maps if "libamdhip64" in line}
     assert len(hip) == 1, hip
+
+
+def _v(lib, ptr, n, st=3 * 2 * 128, sh=128):
+    return ctypes.byref(_lib.Bf16View(ptr, n, st, sh))
+
+
+def test_joint_pack_argument_checks(lib):
+    p = 0x1000
+    f = lib.joy_fused_joint_qkv_pack
+    w = ctypes.c_void_p(p)
+    img = [_v(lib, p, 4) for _ in range(3)]
+    txt = [_v(lib, p, 2) for _ in range(3)]
+    out = [w, w, w]
+    _status(lib, f(*img, *txt, None, None, w, w, 1e-6, 2, 64, *out, None), 1, "requires head_dim=128")
+    _status(lib, f(*img, *txt, _v(lib, p, 3), None, w, w, 1e-6, 2, 128, *out, None), 1,
+            "both be present or both be absent")
+    _status(lib, f(*img, *txt, _v(lib, p, 3), _v(lib, p, 2), w, w, 1e-6, 2, 128, *out, None), 1,
+            "cached K/V lengths must match")
+    _status(lib, f(img[0], _v(lib, p, 3), img[2], *txt, None, None, w, w, 1e-6, 2, 128, *out, None), 1,
+            "image Q/K/V lengths must match")
+    _status(lib, f(*img, _v(lib, p, 0), txt[1], txt[2], None, None, w, w, 1e-6, 2, 128, *out, None), 1,
+            "text Q/K/V lengths must match and be positive")
+    _status(lib, f(*img, *txt, None, None, None, w, 1e-6, 2, 128, *out, None), 1, "weight")
+    _status(lib, f(None, *img[1:], *txt, None, None, w, w, 1e-6, 2, 128, *out, None), 1, "non-null")
+
+
+def test_cached_pack_argument_checks(lib):
+    p = 0x1000
+    f = lib.joy_fused_cached_kv_pack
+    w = ctypes.c_void_p(p)
+    k0 = _v(lib, p, 5)
+    _status(lib, f(k0, k0, None, None, w, w, 2, 256, w, w, None), 1, "requires head_dim=128")
+    _status(lib, f(k0, _v(lib, p, 4), None, None, w, w, 2, 128, w, w, None), 1, "key0/value0 lengths must match")
+    _status(lib, f(k0, k0, k0, None, w, w, 2, 128, w, w, None), 1, "key1 and value1")
+    _status(lib, f(k0, k0, _v(lib, p, 3), _v(lib, p, 2), w, w, 2, 128, w, w, None), 1,
+            "key1/value1 lengths must match and be positive")
+    _status(lib, f(_v(lib, p, 0), _v(lib, p, 0), None, None, w, w, 2, 128, w, w, None), 1,
+            "cache length and heads must be positive")
+    _status(lib, f(k0, k0, None, None, None, w, 2, 128, w, w, None), 1, "cos and sin")
