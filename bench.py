@@ -261,6 +261,98 @@ def bench_pack(steps, warmup):
     return out
 
 
+def bench_norm(steps, warmup):
+    """adaLN LayerNorm + modulation at cfg-4 geometry (M = 10800 tokens, hidden 5120, one
+    broadcast modulation row): the plain op (bf16 out) and the FP8-emitting variant that
+    replaces norm -> bf16 -> per-token quant."""
+    import torch
+    import joyomni_ops as jo
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(4)
+    M, N = L_TOK, E
+    x = torch.randn(M, N, generator=g).to(torch.bfloat16).to(dev)
+    sc = (0.2 * torch.randn(1, N, generator=g)).to(torch.bfloat16).to(dev)
+    sh = (0.2 * torch.randn(1, N, generator=g)).to(torch.bfloat16).to(dev)
+    q = torch.empty(M, N, dtype=torch.float8_e4m3fn, device=dev)
+    s = torch.empty(M, 1, device=dev)
+    out = []
+    t = time_launches(lambda: jo.fused_norm_scale_shift(x, None, None, sc, sh, "layer", 1e-6), steps, warmup)
+    b = 2 * M * N + 2 * M * N + 2 * 2 * N
+    out.append({"op": "fused_norm_scale_shift", "M": M, "N": N, "us": t * 1e6, "gbs": b / t / 1e9,
+                "frac_hbm_peak": b / t / 1e9 / PEAK_HBM_GBS, "algorithmic_bytes": b})
+    t = time_launches(lambda: jo.fused_norm_scale_shift_fp8(x, None, None, sc, sh, "layer", 1e-6, q, s),
+                      steps, warmup)
+    b = 2 * M * N + M * N + 4 * M + 2 * 2 * N
+    out.append({"op": "fused_norm_scale_shift_fp8", "M": M, "N": N, "us": t * 1e6, "gbs": b / t / 1e9,
+                "frac_hbm_peak": b / t / 1e9 / PEAK_HBM_GBS, "algorithmic_bytes": b})
+    return out
+
+
+def bench_block(steps, warmup, n_cached=2):
+    """BASELINE cfg 4: one two-stream MMDiT block's quantised chain, video 10800 + condition 512
+    tokens, hidden 5120, 40 x 128 heads, FFN 13824, random-init weights; the video chunk's K/V go
+    into ring slot 0 and the block attends to ``n_cached`` cached chunks of 10800 tokens read from
+    other ring slots (rotate-on-read). Per-stage device time from HIP events on the launch stream;
+    SDPA is reported separately (excluded from kernel time, included in block latency)."""
+    import torch
+    from joyomni_ops.dit_block import CachedChunk, KVRing, QuantizedDoubleStreamBlock
+    from joyomni_ops.rope import rope_3d_half_tables, rotary_pos_embed_3d
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(5)
+    T_COND, FFN = 512, 13824
+    blk = QuantizedDoubleStreamBlock(E, HEADS, FFN, dev, g)
+    img = torch.randn(1, L_TOK, E, generator=g).to(torch.bfloat16).to(dev)
+    txt = torch.randn(1, T_COND, E, generator=g).to(torch.bfloat16).to(dev)
+    vec = torch.randn(1, E, generator=g).to(torch.bfloat16).to(dev)
+    frames = torch.arange(3 * n_cached, 3 * n_cached + 3)
+    cos, sin = rope_3d_half_tables(3, 45, 80, (44, 42, 42), 10000.0, device=dev, frame_ids=frames)
+    ring = KVRing(RING_SLOTS, L_TOK, HEADS, HEAD_DIM, dev)
+    cached = []
+    for c in range(n_cached):
+        slot = RING_SLOTS - 1 - c
+        ring.k[slot].normal_()
+        ring.v[slot].normal_()
+        ring.lengths[slot] = L_TOK
+        cf, sf = rotary_pos_embed_3d(torch.arange(3 * c, 3 * c + 3), 45, 80, (44, 42, 42), 10000.0)
+        cached.append(CachedChunk(slot, cf.contiguous().to(dev), sf.contiguous().to(dev)))
+    stages = ["qkv", "qkv_norm_rope", "cached_kv", "joint_pack", "attention", "proj_ffn"]
+    stream = torch.cuda.current_stream()
+    ev = {}
+
+    def mark(name):
+        ev[name].record(stream)
+
+    def run(timed):
+        if timed:
+            ev["start"].record(stream)
+        blk.forward(img, txt, vec, cos, sin, ring=ring, write_slot=0, cached=cached,
+                    mark=mark if timed else None)
+
+    for _ in range(warmup):
+        run(False)
+    torch.cuda.synchronize()
+    acc = {k: 0.0 for k in stages}
+    for _ in range(steps):
+        ev = {k: torch.cuda.Event(enable_timing=True) for k in ["start"] + stages}
+        run(True)
+        torch.cuda.synchronize()
+        prev = "start"
+        for k in stages:
+            acc[k] += ev[prev].elapsed_time(ev[k])
+            prev = k
+    per = {k: v / steps for k, v in acc.items()}
+    total = sum(per.values())
+    gemm_flops = 0
+    for M in (L_TOK, T_COND):
+        gemm_flops += 2 * M * (E * 3 * E + E * E + E * FFN + FFN * E)
+    return {"workload": f"cfg4 block: video {L_TOK} + condition {T_COND} tokens, hidden {E}, "
+                        f"{HEADS}x{HEAD_DIM} heads, FFN {FFN}, {n_cached} cached chunks of {L_TOK} tokens",
+            "block_latency_ms": total, "attention_ms": per["attention"],
+            "kernel_ms_excl_attention": total - per["attention"], "stages_ms": per,
+            "gemm_stage_tflops": gemm_flops / ((per["qkv"] + per["proj_ffn"]) / 1e3) / 1e12,
+            "attention_kv_tokens": n_cached * L_TOK + L_TOK + T_COND}
+
+
 def bench_copy(steps, warmup):
     """Plain 1 GiB device-to-device copy: the calibration kernel for the
     FETCH_SIZE / WRITE_SIZE counters (known 1 GiB read + 1 GiB write)."""
@@ -329,7 +421,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time plain launches (no HIP graph)")
-    ap.add_argument("--only", default="all", choices=["all", "qkv", "gemm", "small", "quant", "pack", "copy"])
+    ap.add_argument("--only", default="all",
+                    choices=["all", "qkv", "gemm", "small", "quant", "pack", "norm", "block", "copy"])
     args = ap.parse_args()
     global EAGER
     EAGER = args.eager
@@ -379,6 +472,12 @@ def main():
     if args.only in ("all", "pack"):
         rec["kv_pack"] = bench_pack(args.steps, args.warmup)
         progress("cache read-side packs done")
+    if args.only in ("all", "norm"):
+        rec["adaln_norm"] = bench_norm(args.steps, args.warmup)
+        progress("adaLN norm done")
+    if args.only in ("all", "block"):
+        rec["block_cfg4"] = bench_block(max(3, args.steps // 10), max(1, args.warmup // 5))
+        progress(f"cfg4 block {rec['block_cfg4']['block_latency_ms']:.2f} ms")
     if args.only == "copy":
         rec["copy"] = bench_copy(args.steps, args.warmup)
     if not args.no_cpu:

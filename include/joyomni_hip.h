@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define JOY_ABI_VERSION 2
+#define JOY_ABI_VERSION 3
 
 #if defined(__GNUC__) || defined(__clang__)
 #define JOY_API __attribute__((visibility("default")))
@@ -37,7 +37,9 @@ typedef enum {
   JOY_ERR_HIP = 3               /* the HIP runtime rejected the launch */
 } joy_status;
 
-typedef enum { JOY_DTYPE_BF16 = 0, JOY_DTYPE_FP16 = 1 } joy_dtype;
+typedef enum { JOY_DTYPE_BF16 = 0, JOY_DTYPE_FP16 = 1, JOY_DTYPE_FP32 = 2 } joy_dtype;
+
+typedef enum { JOY_NORM_LAYER = 0, JOY_NORM_RMS = 1 } joy_norm_type;
 
 /* Rounding of the activation quantiser's element step. */
 typedef enum {
@@ -184,6 +186,43 @@ JOY_API joy_status joy_fused_cached_kv_pack(const joy_bf16_view *key0, const joy
                                     const joy_bf16_view *key1, const joy_bf16_view *value1,
                                     const float *cos, const float *sin, int64_t num_heads,
                                     int64_t head_dim, void *out_k, void *out_v, void *stream);
+
+/*
+ * (Layer|RMS)Norm + adaLN scale/shift.
+ * Replaces: fused_norm_scale_shift(Tensor x, Tensor? gamma_opt, Tensor? beta_opt, Tensor scale,
+ *           Tensor shift, int norm_type, float eps) -> Tensor
+ *   schema joyomni_ops/csrc/pybind.cpp:63-65, impl joyomni_ops/csrc/fused_norm_scale_shift.cu:236-275
+ *   (kernel :97-182), called by fused_layernorm_modulate (deploy/xvideo/models/dit/sgl_fused_ops.py:46-91).
+ *   LayerNorm: out = ((x - mean) * rsqrt(var + eps) * gamma + beta) * (1 + scale) + shift
+ *   RMSNorm:   out = (x * rsqrt(mean(x^2) + eps) * gamma) * (1 + scale) + shift
+ * x: [M, N] of dtype (bf16, fp16 or fp32), rows x_row_stride elements apart.
+ * gamma, beta: [N] of dtype or NULL; as in the reference, beta is applied only
+ *   together with gamma (LayerNorm), and gamma without beta means beta = 0.
+ * scale, shift: dense [mod_rows, N] of dtype, mod_rows 1 (broadcast) or M.
+ * out: caller-allocated dense [M, N] of dtype (the reference allocates it).
+ * Reference rules kept: N % 4 == 0, norm_type 0 or 1.
+ */
+JOY_API joy_status joy_fused_norm_scale_shift(const void *x, int64_t x_row_stride, int dtype,
+                                      const void *gamma, const void *beta, const void *scale,
+                                      const void *shift, int64_t mod_rows, void *out, int64_t M,
+                                      int64_t N, int norm_type, float eps, void *stream);
+
+/*
+ * (Layer|RMS)Norm + adaLN scale/shift emitting the per-token FP8 quantisation of
+ * its output (new op, no reference counterpart: it fuses
+ * fused_layernorm_modulate (sgl_fused_ops.py:46-91) with the activation
+ * quantiser of the Fp8Linear that consumes it, fp8_linear.py:38-43 / :57-74).
+ * y = the bf16/fp16 output of joy_fused_norm_scale_shift (same arguments);
+ * output_s[m] = max(absmax_n |y[m, n]|, 1e-8) / 448,
+ * output_q[m, n] = e4m3fn(clamp(y / s)) (JOY_QUANT_DIVIDE) or clamp(y * (1/s)) (JOY_QUANT_RECIPROCAL),
+ * bit-identical to joy_per_token_quant_fp8 applied to y. out (y itself) may be NULL.
+ * dtype must be bf16 or fp16.
+ */
+JOY_API joy_status joy_fused_norm_scale_shift_fp8(const void *x, int64_t x_row_stride, int dtype,
+                                          const void *gamma, const void *beta, const void *scale,
+                                          const void *shift, int64_t mod_rows, void *out,
+                                          void *output_q, float *output_s, int rounding, int64_t M,
+                                          int64_t N, int norm_type, float eps, void *stream);
 
 #ifdef __cplusplus
 }

@@ -225,9 +225,75 @@ joy::RowView row_view(const joy_bf16_view* v) {
 // Largest row count of the pack kernels' grid (16 rows per workgroup).
 constexpr int64_t kMaxPackRows = 0xffffffffLL * 16;
 
+joy_status norm_common(const void* x, int64_t x_row_stride, int dtype, const void* gamma, const void* beta,
+                       const void* scale, const void* shift, int64_t mod_rows, void* out, void* output_q,
+                       float* output_s, int rounding, int64_t M, int64_t N, int norm_type, float eps,
+                       bool fp8, void* stream) {
+  // checks of fused_norm_scale_shift.cu:243-257
+  if (M < 0 || N < 0) return fail(JOY_ERR_INVALID_ARGUMENT, "x must be 2D [M, N]");
+  if (N % 4 != 0) return fail(JOY_ERR_INVALID_ARGUMENT, "N must be divisible by 4");
+  if (mod_rows != 1 && mod_rows != M)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "scale/shift rows must be 1 (broadcast) or M (per-row modulation)");
+  if (norm_type != JOY_NORM_LAYER && norm_type != JOY_NORM_RMS)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "norm_type must be 0 (layer) or 1 (rms)");
+  if (dtype != JOY_DTYPE_BF16 && dtype != JOY_DTYPE_FP16 && dtype != JOY_DTYPE_FP32)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "Unsupported dtype; use float32/float16/bfloat16");
+  if (fp8 && dtype == JOY_DTYPE_FP32)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "the FP8 variant needs bfloat16 or float16 input");
+  if (fp8 && rounding != JOY_QUANT_DIVIDE && rounding != JOY_QUANT_RECIPROCAL)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "rounding must be JOY_QUANT_DIVIDE or JOY_QUANT_RECIPROCAL");
+  if (x_row_stride < N) return fail(JOY_ERR_INVALID_ARGUMENT, "x row stride must be >= N");
+  if (M == 0 || N == 0) return ok();
+  if (!x || !scale || !shift) return fail(JOY_ERR_INVALID_ARGUMENT, "x, scale and shift must be non-null");
+  if (fp8 ? (!output_q || !output_s) : !out)
+    return fail(JOY_ERR_INVALID_ARGUMENT, fp8 ? "output_q and output_s must be non-null" : "out must be non-null");
+  const uintptr_t esz = dtype == JOY_DTYPE_FP32 ? 4 : 2;
+  if (!aligned(x, esz) || !aligned(scale, esz) || !aligned(shift, esz) || (gamma && !aligned(gamma, esz)) ||
+      (beta && !aligned(beta, esz)) || (out && !aligned(out, esz)) || (output_s && !aligned(output_s, 4)))
+    return fail(JOY_ERR_INVALID_ARGUMENT, "tensors must be naturally aligned");
+  joy::NormModArgs a;
+  a.x = x;
+  a.x_stride = x_row_stride;
+  a.gamma = gamma;
+  a.beta = gamma ? beta : nullptr;  // the reference applies beta only with gamma (:125-166)
+  a.scale = scale;
+  a.shift = shift;
+  a.mod_rows = mod_rows;
+  a.out = out;
+  a.out_q = fp8 ? output_q : nullptr;
+  a.out_s = fp8 ? output_s : nullptr;
+  a.M = M;
+  a.N = N;
+  a.dtype = dtype;
+  a.norm_type = norm_type;
+  a.eps = eps;
+  a.divide = rounding == JOY_QUANT_DIVIDE;
+  return hip_status(joy::launch_norm_modulate(a, (hipStream_t)stream),
+                    fp8 ? "fused_norm_scale_shift_fp8 launch" : "fused_norm_scale_shift launch");
+}
+
+
 }  // namespace
 
 extern "C" {
+
+
+joy_status joy_fused_norm_scale_shift(const void* x, int64_t x_row_stride, int dtype, const void* gamma,
+                                      const void* beta, const void* scale, const void* shift,
+                                      int64_t mod_rows, void* out, int64_t M, int64_t N, int norm_type,
+                                      float eps, void* stream) {
+  return norm_common(x, x_row_stride, dtype, gamma, beta, scale, shift, mod_rows, out, nullptr, nullptr,
+                     JOY_QUANT_DIVIDE, M, N, norm_type, eps, false, stream);
+}
+
+joy_status joy_fused_norm_scale_shift_fp8(const void* x, int64_t x_row_stride, int dtype, const void* gamma,
+                                          const void* beta, const void* scale, const void* shift,
+                                          int64_t mod_rows, void* out, void* output_q, float* output_s,
+                                          int rounding, int64_t M, int64_t N, int norm_type, float eps,
+                                          void* stream) {
+  return norm_common(x, x_row_stride, dtype, gamma, beta, scale, shift, mod_rows, out, output_q, output_s,
+                     rounding, M, N, norm_type, eps, true, stream);
+}
 
 joy_status joy_fused_joint_qkv_pack(const joy_bf16_view* img_q, const joy_bf16_view* img_k,
                                     const joy_bf16_view* img_v, const joy_bf16_view* txt_q,

@@ -28,8 +28,13 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   return (b + 0x7fffu + ((b >> 16) & 1u)) >> 16;
 }
 
+typedef __bf16 bf16x2_vt __attribute__((ext_vector_type(2)));
+typedef float f32x2_vt __attribute__((ext_vector_type(2)));
+
+// Two fp32 -> packed bf16 pair, round to nearest even: one v_cvt_pk_bf16_f32 on gfx950.
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+  const f32x2_vt v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_vt));
 }
 
 // fp16 bits -> fp32 (exact).

@@ -75,10 +75,30 @@ struct CachedPackArgs {
   int heads;
 };
 
+// (Layer|RMS)Norm + adaLN scale/shift, optionally + per-token FP8 of the output.
+struct NormModArgs {
+  const void* x;        // [M, N] rows with stride x_stride (elements)
+  int64_t x_stride;
+  const void* gamma;    // [N] or null
+  const void* beta;     // [N] or null (LayerNorm only; used only with gamma)
+  const void* scale;    // [mod_rows, N] dense
+  const void* shift;
+  int64_t mod_rows;     // 1 (broadcast) or M
+  void* out;            // [M, N] dense of the input dtype, or null (FP8 variant only)
+  void* out_q;          // e4m3fn [M, N] or null (plain variant)
+  float* out_s;         // [M]
+  int64_t M, N;
+  int dtype;            // 0 bf16, 1 fp16, 2 fp32
+  int norm_type;        // 0 LayerNorm, 1 RMSNorm
+  float eps;
+  bool divide;          // FP8 rounding: x / s (true) or x * (1/s)
+};
+
 hipError_t launch_per_token_quant(const void* in, bool in_fp16, void* q, float* s, int64_t M,
                                   int64_t K, bool divide, hipStream_t st);
 hipError_t launch_qk_norm_rope(const NormRopeArgs& a, int head_dim, hipStream_t st);
 hipError_t launch_fp8_gemm(const GemmArgs& g, hipStream_t st);
+hipError_t launch_norm_modulate(const NormModArgs& a, hipStream_t st);
 hipError_t launch_joint_qkv_pack(const JointPackArgs& a, hipStream_t st);
 hipError_t launch_cached_kv_pack(const CachedPackArgs& a, hipStream_t st);
 

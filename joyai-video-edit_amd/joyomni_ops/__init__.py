@@ -6,15 +6,16 @@ reference's ``joyomni_ops/joyomni_ops/__init__.py`` (schemas from
 ``from joyomni_ops import ...`` keep working for ``deploy/xvideo``.
 
 The quantised hot path -- ``sgl_per_token_quant_fp8``, ``fp8_scaled_mm``,
-``fused_qk_norm_rope_3d_paired``, the new ``fused_qkv_norm_rope_cache`` and the
-cache read side ``fused_joint_qkv_pack`` / ``fused_cached_kv_pack`` -- runs in
+``fused_qk_norm_rope_3d_paired``, the new ``fused_qkv_norm_rope_cache``, the
+cache read side ``fused_joint_qkv_pack`` / ``fused_cached_kv_pack`` and the
+adaLN ``fused_norm_scale_shift`` (plus its FP8-emitting variant) -- runs in
 hand-written gfx950 kernels of ``libjoyomni_hip.so`` reached through its C ABI
 (``include/joyomni_hip.h``). Importing fails when that library is missing,
 exactly like the reference (``__init__.py:15-19``); nothing falls back.
 
-The two ops outside the quantised path (``fused_norm_scale_shift``,
-``rmsnorm``) keep their reference schemas and are composed from torch device
-ops, so the reference's imports (``sgl_fused_ops.py:27-33``) still resolve.
+``rmsnorm``, which the model never calls, keeps its reference schema as a
+torch device composition, so the reference's imports
+(``sgl_fused_ops.py:27-33``) still resolve.
 """
 from __future__ import annotations
 
@@ -41,6 +42,7 @@ __all__ = [
     "per_token_quant_fp8",
     "fp8_scaled_mm_gelu_tanh",
     "fused_qkv_norm_rope_cache",
+    "fused_norm_scale_shift_fp8",
 ]
 
 _NS = "joyomni_ops"
@@ -72,6 +74,10 @@ _lib_def.define(
 _lib_def.define(
     "fp8_scaled_mm_gelu_tanh(Tensor mat_a, Tensor mat_b, Tensor scales_a, Tensor scales_b, "
     "ScalarType out_dtype, Tensor? bias) -> Tensor")
+_lib_def.define(
+    "fused_norm_scale_shift_fp8(Tensor x, Tensor? gamma_opt, Tensor? beta_opt, Tensor scale, "
+    "Tensor shift, int norm_type, float eps, Tensor(a!) output_q, Tensor(b!) output_s, "
+    "Tensor(c!)? out, bool exact_division) -> ()")
 _lib_def.define(
     "fused_qkv_norm_rope_cache(Tensor qkv, int num_heads, float eps, Tensor q_weight, "
     "Tensor k_weight, Tensor cos, Tensor sin, Tensor(a!) q_out, Tensor(b!)? k_out, "
@@ -384,25 +390,77 @@ def _fused_cached_kv_pack_cuda(key0, value0, key1, value1, cos, sin):
 
 
 # --------------------------------------------------------------------------
-# ops outside the quantised path: torch device compositions of the reference
-# semantics (fused_norm_scale_shift.cu:97-182, rmsnorm.cu:60-84)
+# adaLN norm + modulation (HIP), plain and FP8-emitting
 # --------------------------------------------------------------------------
+_NORM_DTYPE = {torch.bfloat16: _lib.JOY_DTYPE_BF16, torch.float16: _lib.JOY_DTYPE_FP16,
+               torch.float32: _lib.JOY_DTYPE_FP32}
+
+
+def _norm_args(x, gamma_opt, beta_opt, scale, shift, norm_type):
+    # checks of fused_norm_scale_shift.cu:240-262
+    _check(x.is_cuda, "x must be a CUDA tensor")
+    _check(scale.is_cuda, "scale must be a CUDA tensor")
+    _check(shift.is_cuda, "shift must be a CUDA tensor")
+    _check(x.dim() == 2, "x must be 2D [M, N]")
+    _check(x.stride(-1) == 1, "x last dim must be contiguous")
+    M, N = x.shape
+    _check(N % 4 == 0, "N must be divisible by 4")
+    _check(scale.dim() == 2 and shift.dim() == 2, "scale/shift must be 2D [M, N] or [1, N]")
+    _check(scale.size(0) == shift.size(0), "scale/shift row counts must match")
+    _check(scale.size(0) == 1 or scale.size(0) == M,
+           "scale/shift rows must be 1 (broadcast) or M (per-row modulation)")
+    _check(scale.size(1) == N and shift.size(1) == N, "scale/shift last dim must be N")
+    _check(scale.stride(-1) == 1 and shift.stride(-1) == 1, "scale/shift last dim must be contiguous")
+    _check(x.dtype == scale.dtype and x.dtype == shift.dtype, "x/scale/shift dtype must match")
+    _check(norm_type in (0, 1), "norm_type must be 0 (layer) or 1 (rms)")
+    _check(x.dtype in _NORM_DTYPE, "Unsupported dtype; use float32/float16/bfloat16")
+    if gamma_opt is not None:
+        _check(gamma_opt.numel() == N, "gamma must be length N")
+        gamma_opt = gamma_opt.to(x.dtype).contiguous()
+    if beta_opt is not None:
+        _check(beta_opt.numel() == N, "beta must be length N")
+        beta_opt = beta_opt.to(x.dtype).contiguous()
+    # the kernel reads scale/shift rows densely, as the reference kernel does (:112-117)
+    return M, N, gamma_opt, beta_opt, scale.contiguous(), shift.contiguous()
+
+
 @torch.library.impl(_lib_def, "fused_norm_scale_shift", "CUDA")
 def _fused_norm_scale_shift_cuda(x, gamma_opt, beta_opt, scale, shift, norm_type, eps):
-    xf = x.float()
-    if norm_type == 0:
-        y = torch.nn.functional.layer_norm(xf, (x.shape[-1],), eps=eps)
-    elif norm_type == 1:
-        y = xf * torch.rsqrt(xf.square().mean(-1, keepdim=True) + eps)
-    else:
-        raise RuntimeError("norm_type must be 'layer' or 'rms'")
-    if gamma_opt is not None:
-        y = y * gamma_opt.float()
-    if beta_opt is not None:
-        y = y + beta_opt.float()
-    return (y * (1 + scale.float()) + shift.float()).to(x.dtype)
+    M, N, gamma, beta, scale, shift = _norm_args(x, gamma_opt, beta_opt, scale, shift, norm_type)
+    y = torch.empty((M, N), device=x.device, dtype=x.dtype)
+    with torch.cuda.device(x.device):
+        st = _LIB.joy_fused_norm_scale_shift(
+            _ptr(x), x.stride(0) if M > 1 else N, _NORM_DTYPE[x.dtype], _ptr(gamma), _ptr(beta), _ptr(scale),
+            _ptr(shift), scale.size(0), _ptr(y), M, N, int(norm_type), float(eps), _stream(x))
+    _lib.check(_LIB, st)
+    return y
 
 
+@torch.library.impl(_lib_def, "fused_norm_scale_shift_fp8", "CUDA")
+def _fused_norm_scale_shift_fp8_cuda(x, gamma_opt, beta_opt, scale, shift, norm_type, eps, output_q,
+                                     output_s, out, exact_division):
+    M, N, gamma, beta, scale, shift = _norm_args(x, gamma_opt, beta_opt, scale, shift, norm_type)
+    _check(x.dtype in (torch.bfloat16, torch.float16), "x must be bfloat16 or float16")
+    _check(output_q.is_cuda and output_q.is_contiguous() and output_q.dtype == torch.float8_e4m3fn
+           and output_q.shape == (M, N), "output_q must be a contiguous float8_e4m3fn [M, N] CUDA tensor")
+    _check(output_s.is_cuda and output_s.is_contiguous() and output_s.dtype == torch.float32
+           and output_s.numel() == M, "output_s must contain one float32 scale per row")
+    if out is not None:
+        _check(out.is_cuda and out.is_contiguous() and out.dtype == x.dtype and out.shape == (M, N),
+               "out must be a contiguous [M, N] CUDA tensor of x's dtype")
+    rounding = _lib.JOY_QUANT_DIVIDE if exact_division else _lib.JOY_QUANT_RECIPROCAL
+    with torch.cuda.device(x.device):
+        st = _LIB.joy_fused_norm_scale_shift_fp8(
+            _ptr(x), x.stride(0) if M > 1 else N, _NORM_DTYPE[x.dtype], _ptr(gamma), _ptr(beta), _ptr(scale),
+            _ptr(shift), scale.size(0), _ptr(out), _ptr(output_q), _ptr(output_s), rounding, M, N,
+            int(norm_type), float(eps), _stream(x))
+    _lib.check(_LIB, st)
+
+
+# --------------------------------------------------------------------------
+# rmsnorm: outside the quantised path (the model never calls it); a torch
+# device composition of rmsnorm.cu:60-84 keeps the reference import working
+# --------------------------------------------------------------------------
 @torch.library.impl(_lib_def, "rmsnorm", "CUDA")
 def _rmsnorm_cuda(x, weight, eps):
     xf = x.float()
@@ -441,6 +499,12 @@ def _fake_fused_cached_kv_pack(key0, value0, key1, value1, cos, sin):
 @torch.library.register_fake("joyomni_ops::fused_norm_scale_shift")
 def _fake_fused_norm_scale_shift(x, gamma, beta, scale, shift, norm_type, eps):
     return torch.empty_like(x)
+
+
+@torch.library.register_fake("joyomni_ops::fused_norm_scale_shift_fp8")
+def _fake_fused_norm_scale_shift_fp8(x, gamma, beta, scale, shift, norm_type, eps, output_q, output_s,
+                                     out, exact_division):
+    return None
 
 
 @torch.library.register_fake("joyomni_ops::rmsnorm")
@@ -500,6 +564,16 @@ def fused_norm_scale_shift(x, gamma, beta, scale, shift, norm_type, eps=1e-5):
     """Norm(x; gamma, beta) * (1 + scale) + shift. norm_type: 'layer' or 'rms'."""
     nt = 0 if norm_type == "layer" else 1 if norm_type == "rms" else -1
     return _ops.fused_norm_scale_shift(x, gamma, beta, scale, shift, nt, eps)
+
+
+def fused_norm_scale_shift_fp8(x, gamma, beta, scale, shift, norm_type, eps, output_q, output_s,
+                               out=None, exact_division: bool = True):
+    """Norm + adaLN modulation quantised per token to e4m3fn in one pass: output_q/output_s are
+    bit-identical to ``per_token_quant_fp8(fused_norm_scale_shift(...))``; ``out`` optionally
+    receives the modulated row itself."""
+    nt = 0 if norm_type == "layer" else 1 if norm_type == "rms" else -1
+    _ops.fused_norm_scale_shift_fp8(x, gamma, beta, scale, shift, nt, eps, output_q, output_s, out,
+                                    exact_division)
 
 
 def rmsnorm(x, weight, eps=1e-6):

@@ -18,6 +18,10 @@ JOY_ERR_HIP = 3
 
 JOY_DTYPE_BF16 = 0
 JOY_DTYPE_FP16 = 1
+JOY_DTYPE_FP32 = 2
+
+JOY_NORM_LAYER = 0
+JOY_NORM_RMS = 1
 
 JOY_QUANT_DIVIDE = 0
 JOY_QUANT_RECIPROCAL = 1
@@ -55,9 +59,14 @@ SIGNATURES = {
                _vp, _vp, _vp, _vp]),
     "joy_fused_cached_kv_pack": (
         _int, [_view, _view, _view, _view, _vp, _vp, _i64, _i64, _vp, _vp, _vp]),
+    "joy_fused_norm_scale_shift": (
+        _int, [_vp, _i64, _int, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _int, _f32, _vp]),
+    "joy_fused_norm_scale_shift_fp8": (
+        _int, [_vp, _i64, _int, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _int, _i64, _i64, _int, _f32,
+               _vp]),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 class JoyError(RuntimeError):

@@ -1,0 +1,229 @@
+"""Quantised two-stream MMDiT block chain on the gfx950 kernels.
+
+Counterpart of the reference's ``MMDoubleStreamBlock.forward``
+(``deploy/xvideo/models/dit/dit.py:360-558``) with FP8 installed on both streams
+(``dit.py:57-90``) and the streaming KV cache kept as a pre-RoPE ring:
+
+per stream (video "img", condition "txt"), with ``mod = table + vec`` split into
+(shift1, scale1, gate1, shift2, scale2, gate2) (``ModulateWan``, ``dit.py:97-111``):
+
+* adaLN LayerNorm + modulation emitting the QKV input in FP8
+  (``fused_norm_scale_shift_fp8``: ``fused_layernorm_modulate``
+  ``sgl_fused_ops.py:46-91`` fused with the ``Fp8Linear`` quantiser);
+* QKV FP8 GEMM (``fp8_scaled_mm``, ``fp8_linear.py:114-141``);
+* video stream: QKV split + q/k RMSNorm + 3-D RoPE + pre-RoPE K / V into a ring
+  slot in one pass (``fused_qkv_norm_rope_cache``, replacing ``dit.py:409-451`` +
+  ``_write_layer_kv_cache`` ``dit.py:867-882``);
+* cached chunks: pre-RoPE K rotated on read straight out of their ring slots
+  with fp32 full-width tables (``fused_cached_kv_pack``, ``_concat_kv_entries``
+  ``dit.py:216-271``);
+* joint Q/K/V pack with the condition stream's two-rounding q/k RMSNorm
+  (``fused_joint_qkv_pack``, ``dit.py:489-496``);
+* attention: PyTorch SDPA, non-causal, no mask (``dit.py:154-167``), restricted to
+  its fused flash / memory-efficient kernels;
+* out-proj FP8 GEMM and gated residual (``fused_add_gate``, ``dit.py:525-528``);
+* adaLN + FP8 quant -> FFN-up FP8 GEMM with the GELU-tanh epilogue -> quant ->
+  FFN-down FP8 GEMM -> gated residual (``dit.py:508-513,529-538``).
+
+Activation quantiser rounding per K follows the reference's ROCm path
+(``fp8_linear.py:57-74``): reciprocal-multiply below K = 8192, division above.
+Weights are random-initialised with the BASELINE distributions (there are no
+checkpoints here): Linear weights N(0, 0.02), biases N(0, 0.01), q/k norm weights
+N(1, 0.1), modulation table N(0, 1)/sqrt(hidden) (``ModulateWan.__init__``).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Callable, List, Optional, Sequence, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import (fused_cached_kv_pack, fused_joint_qkv_pack, fused_norm_scale_shift_fp8,
+               fused_qkv_norm_rope_cache)
+from .fp8_linear import Fp8Linear, exact_division_for
+
+NORM_EPS = 1e-6            # dit.py:35
+NUM_MODULATION_CHUNKS = 6  # dit.py:37
+
+
+@dataclass
+class StreamWeights:
+    """One stream's parameters (bf16 originals kept for reference checks)."""
+    mod_table: torch.Tensor       # [1, 6, E] bf16
+    q_norm: torch.Tensor          # [D] bf16
+    k_norm: torch.Tensor          # [D] bf16
+    linears: dict                 # name -> nn.Linear (bf16): qkv, proj, up, down
+    qkv: Fp8Linear = None
+    proj: Fp8Linear = None
+    up: Fp8Linear = None
+    down: Fp8Linear = None
+
+
+def random_stream_weights(hidden: int, heads: int, mlp_hidden: int, generator: torch.Generator,
+                          device) -> StreamWeights:
+    """Random-init weights of one stream with the BASELINE distributions (drawn on the CPU)."""
+    D = hidden // heads
+
+    def linear(k_in, k_out):
+        lin = nn.Linear(k_in, k_out, bias=True)
+        with torch.no_grad():
+            lin.weight.copy_(torch.randn(k_out, k_in, generator=generator) * 0.02)
+            lin.bias.copy_(torch.randn(k_out, generator=generator) * 0.01)
+        return lin.to(torch.bfloat16).to(device)
+
+    table = (torch.randn(1, NUM_MODULATION_CHUNKS, hidden, generator=generator) / hidden ** 0.5)
+    w = StreamWeights(
+        mod_table=table.to(torch.bfloat16).to(device),
+        q_norm=(1 + 0.1 * torch.randn(D, generator=generator)).to(torch.bfloat16).to(device),
+        k_norm=(1 + 0.1 * torch.randn(D, generator=generator)).to(torch.bfloat16).to(device),
+        linears={"qkv": linear(hidden, 3 * hidden), "proj": linear(hidden, hidden),
+                 "up": linear(hidden, mlp_hidden), "down": linear(mlp_hidden, hidden)})
+    return w
+
+
+class KVRing:
+    """Bounded KV-state cache: pre-RoPE K and V of up to ``slots`` chunks, ``[slots, capacity, H, D]``
+    bf16 each, caller-owned and written in place (the reference keeps the same content in a dict of
+    per-chunk tensors, ``dit.py:715-894``)."""
+
+    def __init__(self, slots: int, capacity: int, heads: int, head_dim: int, device):
+        self.k = torch.zeros(slots, capacity, heads, head_dim, dtype=torch.bfloat16, device=device)
+        self.v = torch.zeros_like(self.k)
+        self.lengths = [0] * slots
+
+    def key(self, slot: int) -> torch.Tensor:
+        return self.k[slot, : self.lengths[slot]][None]
+
+    def value(self, slot: int) -> torch.Tensor:
+        return self.v[slot, : self.lengths[slot]][None]
+
+
+@dataclass
+class CachedChunk:
+    """A cached chunk to attend to: its ring slot and the fp32 full-width RoPE tables
+    ``[len, D]`` of its window-relative positions (``dit.py:1196-1217``)."""
+    slot: int
+    cos: torch.Tensor
+    sin: torch.Tensor
+
+
+class QuantizedDoubleStreamBlock:
+    """The quantised chain of one two-stream MMDiT block (see the module docstring)."""
+
+    def __init__(self, hidden: int, heads: int, mlp_hidden: int, device, generator: torch.Generator,
+                 quant_rounding: str = "reference_rocm"):
+        self.hidden, self.heads, self.mlp_hidden = hidden, heads, mlp_hidden
+        self.head_dim = hidden // heads
+        self.quant_rounding = quant_rounding
+        self.img = random_stream_weights(hidden, heads, mlp_hidden, generator, device)
+        self.txt = random_stream_weights(hidden, heads, mlp_hidden, generator, device)
+        for w in (self.img, self.txt):
+            w.qkv = Fp8Linear.from_linear(w.linears["qkv"], quant_rounding=quant_rounding)
+            w.proj = Fp8Linear.from_linear(w.linears["proj"], quant_rounding=quant_rounding)
+            w.up = Fp8Linear.from_linear(w.linears["up"], gelu_tanh=True, quant_rounding=quant_rounding)
+            w.down = Fp8Linear.from_linear(w.linears["down"], quant_rounding=quant_rounding)
+
+    # -- pieces -------------------------------------------------------------
+    @staticmethod
+    def modulation(w: StreamWeights, vec: torch.Tensor) -> List[torch.Tensor]:
+        """ModulateWan.forward (dit.py:103-106): [1, 6, E] + vec -> six [1, E] rows."""
+        return [c.squeeze(1) for c in (w.mod_table + vec.unsqueeze(1)).chunk(NUM_MODULATION_CHUNKS, dim=1)]
+
+    def norm_quant(self, x2d: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor, k_in: int):
+        """LayerNorm + (1 + scale) + shift, quantised per token for the next Fp8Linear."""
+        M = x2d.shape[0]
+        q = torch.empty(M, x2d.shape[1], dtype=torch.float8_e4m3fn, device=x2d.device)
+        s = torch.empty(M, 1, dtype=torch.float32, device=x2d.device)
+        fused_norm_scale_shift_fp8(x2d, None, None, scale, shift, "layer", NORM_EPS, q, s, None,
+                                   exact_division_for(k_in, self.quant_rounding))
+        return q, s
+
+    @staticmethod
+    def gated_residual(x: torch.Tensor, y: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
+        """fused_add_gate (sgl_fused_ops.py:302-305): x + y * gate."""
+        return torch.addcmul(x, y, gate.unsqueeze(1))
+
+    @staticmethod
+    def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+        """SDPA on [B, S, H, D] operands (dit.py:154-167), fused kernels only."""
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            out = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
+                                                 is_causal=False)
+        return out.transpose(1, 2)
+
+    # -- forward ------------------------------------------------------------
+    def forward(self, img: torch.Tensor, txt: torch.Tensor, vec: torch.Tensor, img_cos: torch.Tensor,
+                img_sin: torch.Tensor, ring: Optional[KVRing] = None, write_slot: Optional[int] = None,
+                cached: Sequence[CachedChunk] = (), mark: Optional[Callable[[str], None]] = None
+                ) -> Tuple[torch.Tensor, torch.Tensor]:
+        """img [1, L, E], txt [1, T, E], vec [1, E] bf16; img_cos/img_sin bf16 half tables [L, D/2].
+
+        Writes the video chunk's pre-RoPE K and V into ``ring`` slot ``write_slot`` (if given) and
+        attends to [cached chunks | video | condition]. ``mark(name)`` is called after each stage
+        (used by the benchmark to place timing events). Returns the updated (img, txt).
+        """
+        mark = mark or (lambda name: None)
+        E, H, D = self.hidden, self.heads, self.head_dim
+        L, T = img.shape[1], txt.shape[1]
+        img2, txt2 = img.reshape(L, E), txt.reshape(T, E)
+        im = self.modulation(self.img, vec)
+        tm = self.modulation(self.txt, vec)
+
+        # QKV projections
+        q8, s8 = self.norm_quant(img2, im[0], im[1], E)
+        img_qkv = self.img.qkv.gemm(q8, s8)
+        q8, s8 = self.norm_quant(txt2, tm[0], tm[1], E)
+        txt_qkv = self.txt.qkv.gemm(q8, s8)
+        mark("qkv")
+
+        # video q/k norm + RoPE, pre-RoPE K / V into the ring
+        img_q = torch.empty(L, H, D, dtype=torch.bfloat16, device=img.device)
+        img_k = torch.empty_like(img_q)
+        if ring is not None and write_slot is not None:
+            fused_qkv_norm_rope_cache(img_qkv, H, NORM_EPS, self.img.q_norm, self.img.k_norm, img_cos, img_sin,
+                                      img_q, img_k, ring.k, ring.v, write_slot, 0)
+            ring.lengths[write_slot] = L
+        else:
+            fused_qkv_norm_rope_cache(img_qkv, H, NORM_EPS, self.img.q_norm, self.img.k_norm, img_cos, img_sin,
+                                      img_q, img_k, None, None, 0, 0)
+        mark("qkv_norm_rope")
+
+        # cached chunks rotated on read (one or two segments per launch, as the reference)
+        cached_k = cached_v = None
+        if cached:
+            parts_k, parts_v = [], []
+            for i in range(0, len(cached), 2):
+                seg = cached[i:i + 2]
+                cos = torch.cat([c.cos for c in seg]) if len(seg) > 1 else seg[0].cos
+                sin = torch.cat([c.sin for c in seg]) if len(seg) > 1 else seg[0].sin
+                k1 = ring.key(seg[1].slot) if len(seg) > 1 else None
+                v1 = ring.value(seg[1].slot) if len(seg) > 1 else None
+                pk, pv = fused_cached_kv_pack(ring.key(seg[0].slot), ring.value(seg[0].slot), k1, v1, cos, sin)
+                parts_k.append(pk)
+                parts_v.append(pv)
+            cached_k = parts_k[0] if len(parts_k) == 1 else torch.cat(parts_k, dim=1)
+            cached_v = parts_v[0] if len(parts_v) == 1 else torch.cat(parts_v, dim=1)
+        mark("cached_kv")
+
+        # joint Q / K / V
+        iv = img_qkv.view(1, L, 3, H, D)
+        tv = txt_qkv.view(1, T, 3, H, D)
+        q, k, v = fused_joint_qkv_pack(img_q[None], img_k[None], iv[:, :, 2], tv[:, :, 0], tv[:, :, 1],
+                                       tv[:, :, 2], cached_k, cached_v, self.txt.q_norm, self.txt.k_norm,
+                                       NORM_EPS)
+        mark("joint_pack")
+        attn = self.attention(q, k, v).flatten(2, 3)
+        mark("attention")
+
+        outs = []
+        for x2d, w, m, a in ((img2, self.img, im, attn[0, :L]), (txt2, self.txt, tm, attn[0, L:])):
+            x = self.gated_residual(x2d[None], w.proj(a)[None], m[2])[0]
+            q8, s8 = self.norm_quant(x, m[3], m[4], E)
+            h = w.up.gemm(q8, s8)
+            x = self.gated_residual(x[None], w.down(h)[None], m[5])[0]
+            outs.append(x)
+        mark("proj_ffn")
+        return outs[0].reshape(1, L, E), outs[1].reshape(1, T, E)

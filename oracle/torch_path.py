@@ -63,3 +63,112 @@ def fp8_linear(x: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor, bias: torc
     a = q.float() * s
     b = w_q.float() * w_s.reshape(-1, 1)
     return (a @ b.t() + bias.float()).to(torch.bfloat16)
+
+
+# ---------------------------------------------------------------------------
+# One two-stream MMDiT block (MMDoubleStreamBlock.forward, dit.py:360-558), CPU
+# ---------------------------------------------------------------------------
+def quantize_per_token_rounding(x: torch.Tensor, exact_division: bool):
+    """fp8_linear.py:38-43 (division) or per_token_quant_fp8_rocm.hip:72-77 (reciprocal)."""
+    absmax = x.abs().amax(dim=1, keepdim=True).float().clamp_min(1e-8)
+    scale = absmax / FP8_MAX
+    v = x.float() / scale if exact_division else x.float() * (1.0 / scale)
+    return v.clamp(-FP8_MAX, FP8_MAX).to(FP8), scale
+
+
+def _fp8_linear_ref(x2d, w_q, w_s, bias, exact_division, gelu=False):
+    q, s = quantize_per_token_rounding(x2d, exact_division)
+    y = ((q.float() * s) @ (w_q.float() * w_s.reshape(-1, 1)).t() + bias.float()).to(torch.bfloat16)
+    if gelu:  # F.gelu on the bf16 GEMM output (dit.py:87-89)
+        y = torch.nn.functional.gelu(y.float(), approximate="tanh").to(torch.bfloat16)
+    return y
+
+
+def _layernorm_modulate_ref(x2d, shift, scale, eps):
+    """fused_norm_scale_shift.cu:97-182 without affine weights: fp32, one rounding."""
+    y = torch.nn.functional.layer_norm(x2d.float(), (x2d.shape[1],), eps=eps)
+    return (y * (1 + scale.float()) + shift.float()).to(torch.bfloat16)
+
+
+def _rope_half(x, cos_half, sin_half):
+    """Interleaved-pair rotation with half tables [L, D/2] (fused_qknorm_rope_3d_kernel.cu:95-104)."""
+    c = cos_half.float()[:, None, :]
+    s = sin_half.float()[:, None, :]
+    x0, x1 = x[..., 0::2], x[..., 1::2]
+    out = torch.empty_like(x)
+    out[..., 0::2] = x0 * c - x1 * s
+    out[..., 1::2] = x0 * s + x1 * c
+    return out
+
+
+def _rms_two_round(x, w, eps):
+    xf = x.float()
+    n = (xf * torch.rsqrt(xf.square().mean(-1, keepdim=True) + eps)).to(torch.bfloat16)
+    return (n.float() * w.float()).to(torch.bfloat16)
+
+
+def double_stream_block(img, txt, vec, streams, heads, img_cos_half, img_sin_half, cached=(),
+                        division_min_k=8192, eps=1e-6):
+    """The quantised block chain on the CPU, with the reference's numerics at every step.
+
+    img [L, E], txt [T, E], vec [1, E] bf16; ``streams`` = (img_w, txt_w) dicts with bf16
+    ``mod_table`` [1, 6, E], ``q_norm``/``k_norm`` [D] and per linear ``<name>_q`` [N, K] e4m3fn,
+    ``<name>_s`` [N] fp32, ``<name>_b`` [N] bf16 for qkv, proj, up, down; ``cached`` = list of
+    (key_pre_rope [len, H, D] bf16, value [len, H, D] bf16, cos_full [len, D] f32, sin_full).
+    Returns (img_out, txt_out, k_pre_img, v_img).
+    """
+    L, E = img.shape
+    T = txt.shape[0]
+    D = E // heads
+    outs = {}
+    qkvs = []
+    for x, w in ((img, streams[0]), (txt, streams[1])):
+        mod = [c.squeeze(1) for c in (w["mod_table"].float() + vec.float().unsqueeze(1)).to(torch.bfloat16)
+               .chunk(6, dim=1)]
+        xm = _layernorm_modulate_ref(x, mod[0], mod[1], eps)
+        qkv = _fp8_linear_ref(xm, w["qkv_q"], w["qkv_s"], w["qkv_b"], E >= division_min_k)
+        qkvs.append((qkv, mod))
+    # video: q/k RMSNorm (one rounding) + RoPE; pre-RoPE K kept
+    qkv_i = qkvs[0][0].view(L, 3, heads, D)
+    wi, wt = streams
+    qi, ki, vi = qkv_i[:, 0], qkv_i[:, 1], qkv_i[:, 2]
+
+    def norm1(x, wn):
+        xf = x.float()
+        return xf * torch.rsqrt(xf.square().mean(-1, keepdim=True) + eps) * wn.float()
+
+    qh, kh = norm1(qi, wi["q_norm"]), norm1(ki, wi["k_norm"])
+    q_img = _rope_half(qh, img_cos_half, img_sin_half).to(torch.bfloat16)
+    k_img = _rope_half(kh, img_cos_half, img_sin_half).to(torch.bfloat16)
+    k_pre = kh.to(torch.bfloat16)
+    # condition: two-rounding q/k RMSNorm, no RoPE (fused_joint_qkv_pack.cu:58-79)
+    qkv_t = qkvs[1][0].view(T, 3, heads, D)
+    q_txt = _rms_two_round(qkv_t[:, 0], wt["q_norm"], eps)
+    k_txt = _rms_two_round(qkv_t[:, 1], wt["k_norm"], eps)
+    # cached chunks rotated with fp32 full-width tables (fused_joint_qkv_pack.cu:207-218)
+    ck, cv = [], []
+    for key, value, cos, sin in cached:
+        kf = key.float()
+        c = cos.float()[:, None, 0::2]
+        s = sin.float()[:, None, 0::2]
+        out = torch.empty_like(kf)
+        out[..., 0::2] = kf[..., 0::2] * c - kf[..., 1::2] * s
+        out[..., 1::2] = kf[..., 0::2] * s + kf[..., 1::2] * c
+        ck.append(out.to(torch.bfloat16))
+        cv.append(value)
+    Q = torch.cat([q_img, q_txt])
+    K = torch.cat(ck + [k_img, k_txt])
+    V = torch.cat(cv + [vi, qkv_t[:, 2]])
+    attn = torch.nn.functional.scaled_dot_product_attention(
+        Q.float().transpose(0, 1)[None], K.float().transpose(0, 1)[None], V.float().transpose(0, 1)[None])
+    attn = attn[0].transpose(0, 1).reshape(L + T, E).to(torch.bfloat16)
+    res = []
+    for (x, w, (qkv, mod), a) in ((img, wi, qkvs[0], attn[:L]), (txt, wt, qkvs[1], attn[L:])):
+        p = _fp8_linear_ref(a, w["proj_q"], w["proj_s"], w["proj_b"], E >= division_min_k)
+        x = (x.float() + p.float() * mod[2].float()).to(torch.bfloat16)
+        xm = _layernorm_modulate_ref(x, mod[3], mod[4], eps)
+        h = _fp8_linear_ref(xm, w["up_q"], w["up_s"], w["up_b"], E >= division_min_k, gelu=True)
+        d = _fp8_linear_ref(h, w["down_q"], w["down_s"], w["down_b"], h.shape[1] >= division_min_k)
+        x = (x.float() + d.float() * mod[5].float()).to(torch.bfloat16)
+        res.append(x)
+    return res[0], res[1], k_pre, vi.contiguous()

@@ -134,3 +134,19 @@ def test_cached_pack_argument_checks(lib):
     _status(lib, f(_v(lib, p, 0), _v(lib, p, 0), None, None, w, w, 2, 128, w, w, None), 1,
             "cache length and heads must be positive")
     _status(lib, f(k0, k0, None, None, None, w, 2, 128, w, w, None), 1, "cos and sin")
+
+
+def test_norm_argument_checks(lib):
+    p = ctypes.c_void_p(0x1000)
+    f = lib.joy_fused_norm_scale_shift
+    _status(lib, f(p, 64, 0, None, None, p, p, 1, p, 4, 62, 0, 1e-6, None), 1, "divisible by 4")
+    _status(lib, f(p, 64, 0, None, None, p, p, 2, p, 4, 64, 0, 1e-6, None), 1, "broadcast")
+    _status(lib, f(p, 64, 0, None, None, p, p, 1, p, 4, 64, 3, 1e-6, None), 1, "norm_type")
+    _status(lib, f(p, 64, 9, None, None, p, p, 1, p, 4, 64, 0, 1e-6, None), 1, "Unsupported dtype")
+    _status(lib, f(p, 32, 0, None, None, p, p, 1, p, 4, 64, 0, 1e-6, None), 1, "row stride")
+    assert f(None, 64, 0, None, None, None, None, 1, None, 0, 64, 0, 1e-6, None) == 0
+    g = lib.joy_fused_norm_scale_shift_fp8
+    _status(lib, g(p, 64, 2, None, None, p, p, 1, None, p, p, 0, 4, 64, 0, 1e-6, None), 1,
+            "bfloat16 or float16")
+    _status(lib, g(p, 64, 0, None, None, p, p, 1, None, p, p, 7, 4, 64, 0, 1e-6, None), 1, "rounding")
+    _status(lib, g(p, 64, 0, None, None, p, p, 1, None, None, p, 0, 4, 64, 0, 1e-6, None), 1, "output_q")

@@ -62,7 +62,10 @@ def assert_acc_bound(y_bits, qa, qw, sa, sw, bias, what):
 
 
 @pytest.mark.parametrize("M,N,K", [(300, 264, 256), (256, 256, 128), (33, 40, 48), (1, 8, 16),
-                                   (513, 520, 384), (64, 1024, 4096)])
+                                   (513, 520, 384), (64, 1024, 4096),
+                                   # small-M (skinny) kernel: one row, fewer 128-byte K chunks
+                                   # than waves, uneven chunks per wave, partial column tiles
+                                   (1, 520, 384), (65, 72, 1280), (200, 4104, 640), (256, 15360, 128)])
 def test_exact_small_integers_bit_exact(M, N, K):
     """fp8 integers in [-8, 8] and power-of-two scales: every partial sum is exact,
     so the output is fixed to the last bit whatever the summation order."""

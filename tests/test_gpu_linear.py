@@ -11,12 +11,15 @@ from oracle.fp8 import bf16_to_f32
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("gelu", [False, True])
-def test_fp8_linear_matches_oracle(gelu):
-    announce("Fp8Linear", gelu)
+@pytest.mark.parametrize("gelu,rounding,K", [(False, "reference_rocm", 1024), (True, "reference_rocm", 1024),
+                                             (False, "reference_rocm", 8192), (False, "division", 1024)])
+def test_fp8_linear_matches_oracle(gelu, rounding, K):
+    """Activation rounding as the reference's ROCm path (fp8_linear.py:57-74): reciprocal-multiply
+    below K = 8192, division from 8192 up; or division for every K."""
+    announce("Fp8Linear", gelu, rounding, K)
     from joyomni_ops.fp8_linear import Fp8Linear, _quantize_weight_per_channel
     g = gen(21)
-    K, N = 1024, 768
+    N = 768
     lin = torch.nn.Linear(K, N, bias=True)
     with torch.no_grad():
         lin.weight.copy_(torch.randn(N, K, generator=g) * 0.02)
@@ -25,11 +28,13 @@ def test_fp8_linear_matches_oracle(gelu):
     wq, ws = _quantize_weight_per_channel(lin.weight.data)
     qw_ref, sw_ref = oq.quant_weight_per_channel(u16(lin.weight.data))
     assert np.array_equal(u8(wq.t()), qw_ref) and np.array_equal(ws.cpu().numpy().reshape(-1), sw_ref)
-    layer = Fp8Linear.from_linear(lin, gelu_tanh=gelu)
+    layer = Fp8Linear.from_linear(lin, gelu_tanh=gelu, quant_rounding=rounding)
+    variant = "div" if (rounding == "division" or K >= 8192) else "rcp"
+    assert layer.exact_division == (variant == "div")
     x = outlier_acts(2 * 150, K, g).reshape(2, 150, K)
     y = layer(x.to(DEV))
     assert y.shape == (2, 150, N)
-    qa, sa = oq.quant_per_token(u16(x.reshape(-1, K)), "bf16", "div")
+    qa, sa = oq.quant_per_token(u16(x.reshape(-1, K)), "bf16", variant)
     pre = og.reference_fp32(qa, qw_ref, sa, sw_ref, u16(lin.bias.data))
     rms = float(np.sqrt(np.mean(pre.astype(np.float64) ** 2)))
     got = y.float().cpu().numpy().reshape(-1, N)
