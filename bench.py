@@ -51,6 +51,28 @@ def quant_bytes(M, K) -> int:
 
 EAGER = False  # --eager: plain launches instead of one HIP graph (for counter runs)
 
+# MI355X has a 256 MiB memory-side cache (MALL) in front of HBM: a launch whose working set fits
+# in it, replayed on the same buffers, is partly served from it. Memory-bound benchmarks whose
+# working set is smaller than this cycle through enough independent buffer sets that each set
+# is evicted before it is used again.
+MALL_BYTES = 256 << 20
+
+
+def buffer_sets(bytes_per_set: int) -> int:
+    """Number of buffer sets so that the sets together span >= 3 x the MALL."""
+    return max(1, -(-3 * MALL_BYTES // max(1, bytes_per_set)))
+
+
+class Rotation:
+    """Calls fn(set) on successive sets; each call during graph capture bakes in its own set."""
+
+    def __init__(self, sets, fn):
+        self.sets, self.fn, self.i = sets, fn, 0
+
+    def __call__(self):
+        self.fn(self.sets[self.i % len(self.sets)])
+        self.i += 1
+
 
 def time_launches(fn, steps: int, warmup: int):
     """Average per-launch time (s) of `fn` (one kernel launch) over `steps` launches.
@@ -185,6 +207,8 @@ def bench_gemm(steps, warmup):
 
 
 def bench_small_m(steps, warmup):
+    """cfg 3: the weights dominate the bytes; each launch reads a different copy of W (as
+    consecutive layers do), so W streams from HBM rather than from the MALL."""
     import torch
     import joyomni_ops as jo
     dev = torch.device("cuda:0")
@@ -193,20 +217,24 @@ def bench_small_m(steps, warmup):
         K = 5120
         g = torch.Generator().manual_seed(N)
         w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).to(dev)
-        qw = torch.empty(N, K, dtype=torch.float8_e4m3fn, device=dev)
+        qw0 = torch.empty(N, K, dtype=torch.float8_e4m3fn, device=dev)
         sw = torch.empty(N, 1, device=dev)
-        jo.per_token_quant_fp8(w, qw, sw, True)
+        jo.per_token_quant_fp8(w, qw0, sw, True)
+        del w
+        weights = [qw0] + [qw0.clone() for _ in range(buffer_sets(N * K) - 1)]
         bias = torch.zeros(N, dtype=torch.bfloat16, device=dev)
         for M in SMALL_M:
             x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
             qa = torch.empty(M, K, dtype=torch.float8_e4m3fn, device=dev)
             sa = torch.empty(M, 1, device=dev)
             jo.per_token_quant_fp8(x, qa, sa, True)
-            t = time_launches(lambda: jo.fp8_scaled_mm(qa, qw.t(), sa, sw.reshape(1, N), torch.bfloat16, bias),
-                              steps, warmup)
+            step = Rotation(weights, lambda qw: jo.fp8_scaled_mm(qa, qw.t(), sa, sw.reshape(1, N),
+                                                                 torch.bfloat16, bias))
+            t = time_launches(step, steps, warmup)
             b = gemm_bytes(M, N, K)
             out.append({"M": M, "K": K, "N": N, "us": t * 1e6, "gbs": b / t / 1e9,
-                        "frac_hbm_peak": b / t / 1e9 / PEAK_HBM_GBS})
+                        "frac_hbm_peak": b / t / 1e9 / PEAK_HBM_GBS, "weight_copies": len(weights)})
+        del weights
     return out
 
 
@@ -217,12 +245,15 @@ def bench_quant(steps, warmup):
     out = []
     for K in (5120, 13824):
         M = L_TOK
-        x = torch.randn(M, K, generator=torch.Generator().manual_seed(K)).to(torch.bfloat16).to(dev)
-        q = torch.empty(M, K, dtype=torch.float8_e4m3fn, device=dev)
-        s = torch.empty(M, 1, device=dev)
-        t = time_launches(lambda: jo.per_token_quant_fp8(x, q, s, True), steps, warmup)
         b = quant_bytes(M, K)
-        out.append({"M": M, "K": K, "us": t * 1e6, "gbs": b / t / 1e9, "frac_hbm_peak": b / t / 1e9 / PEAK_HBM_GBS})
+        x0 = torch.randn(M, K, generator=torch.Generator().manual_seed(K)).to(torch.bfloat16).to(dev)
+        sets = [(x0 if i == 0 else x0.clone(), torch.empty(M, K, dtype=torch.float8_e4m3fn, device=dev),
+                 torch.empty(M, 1, device=dev)) for i in range(buffer_sets(b))]
+        t = time_launches(Rotation(sets, lambda st: jo.per_token_quant_fp8(st[0], st[1], st[2], True)),
+                          steps, warmup)
+        out.append({"M": M, "K": K, "us": t * 1e6, "gbs": b / t / 1e9, "frac_hbm_peak": b / t / 1e9 / PEAK_HBM_GBS,
+                    "buffer_sets": len(sets)})
+        del sets, x0
     return out
 
 
@@ -264,27 +295,32 @@ def bench_pack(steps, warmup):
 def bench_norm(steps, warmup):
     """adaLN LayerNorm + modulation at cfg-4 geometry (M = 10800 tokens, hidden 5120, one
     broadcast modulation row): the plain op (bf16 out) and the FP8-emitting variant that
-    replaces norm -> bf16 -> per-token quant."""
+    replaces norm -> bf16 -> per-token quant. Buffer sets rotate past the MALL."""
     import torch
     import joyomni_ops as jo
     dev = torch.device("cuda:0")
     g = torch.Generator().manual_seed(4)
     M, N = L_TOK, E
-    x = torch.randn(M, N, generator=g).to(torch.bfloat16).to(dev)
+    x0 = torch.randn(M, N, generator=g).to(torch.bfloat16).to(dev)
     sc = (0.2 * torch.randn(1, N, generator=g)).to(torch.bfloat16).to(dev)
     sh = (0.2 * torch.randn(1, N, generator=g)).to(torch.bfloat16).to(dev)
-    q = torch.empty(M, N, dtype=torch.float8_e4m3fn, device=dev)
-    s = torch.empty(M, 1, device=dev)
     out = []
-    t = time_launches(lambda: jo.fused_norm_scale_shift(x, None, None, sc, sh, "layer", 1e-6), steps, warmup)
     b = 2 * M * N + 2 * M * N + 2 * 2 * N
-    out.append({"op": "fused_norm_scale_shift", "M": M, "N": N, "us": t * 1e6, "gbs": b / t / 1e9,
-                "frac_hbm_peak": b / t / 1e9 / PEAK_HBM_GBS, "algorithmic_bytes": b})
-    t = time_launches(lambda: jo.fused_norm_scale_shift_fp8(x, None, None, sc, sh, "layer", 1e-6, q, s),
+    xs = [x0] + [x0.clone() for _ in range(buffer_sets(b) - 1)]
+    t = time_launches(Rotation(xs, lambda x: jo.fused_norm_scale_shift(x, None, None, sc, sh, "layer", 1e-6)),
                       steps, warmup)
-    b = 2 * M * N + M * N + 4 * M + 2 * 2 * N
-    out.append({"op": "fused_norm_scale_shift_fp8", "M": M, "N": N, "us": t * 1e6, "gbs": b / t / 1e9,
-                "frac_hbm_peak": b / t / 1e9 / PEAK_HBM_GBS, "algorithmic_bytes": b})
+    out.append({"op": "fused_norm_scale_shift", "M": M, "N": N, "us": t * 1e6, "gbs": b / t / 1e9,
+                "frac_hbm_peak": b / t / 1e9 / PEAK_HBM_GBS, "algorithmic_bytes": b, "buffer_sets": len(xs)})
+    for exact in (False, True):
+        b = 2 * M * N + M * N + 4 * M + 2 * 2 * N
+        sets = [(x, torch.empty(M, N, dtype=torch.float8_e4m3fn, device=dev), torch.empty(M, 1, device=dev))
+                for x in xs[:buffer_sets(b)]]
+        t = time_launches(Rotation(sets, lambda st: jo.fused_norm_scale_shift_fp8(
+            st[0], None, None, sc, sh, "layer", 1e-6, st[1], st[2], None, exact)), steps, warmup)
+        out.append({"op": "fused_norm_scale_shift_fp8", "rounding": "division" if exact else "reciprocal",
+                    "M": M, "N": N, "us": t * 1e6, "gbs": b / t / 1e9,
+                    "frac_hbm_peak": b / t / 1e9 / PEAK_HBM_GBS, "algorithmic_bytes": b, "buffer_sets": len(sets)})
+        del sets
     return out
 
 
