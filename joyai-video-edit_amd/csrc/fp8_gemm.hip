@@ -304,10 +304,13 @@ __device__ __forceinline__ void sched_pattern() {
 // nobody reads again) and the extra fragment read is discarded, so every iteration
 // waits on the same constant vmcnt.
 //
-// Tile source. Bulk launch (sub_log2 < 0): block b takes position
+// Tile source. Bulk launch (sub_log2 == -1): block b takes position
 // xcd_position(b) of the grouped 256x256 tile order, positions [0, gridDim.x).
 // Tail launch (sub_log2 >= 0): block b takes sub-tile (b mod 2^sub_log2) of the
 // 256x256 tile at position tile_base + (b >> sub_log2).
+// Small-M launch (sub_log2 == -2): BM x BN tiles of a tiles_m x tiles_n grid,
+// M fastest within each XCD's contiguous range (the M tiles of one weight tile
+// run together, so W is fetched once per XCD).
 // ---------------------------------------------------------------------------
 template <bool kBf16, bool kGelu, int BM, int BN, int S>
 __global__ __launch_bounds__(256, 1) void fp8_gemm_4w(
@@ -332,7 +335,11 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4w(
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   int m0, n0;
-  if (sub_log2 < 0) {
+  if (sub_log2 == -2) {
+    const TileCoord tc = map_tile(blockIdx.x, gridDim.x, tiles_n, tiles_m, 1, 0);
+    m0 = tc.tn * BM;
+    n0 = tc.tm * BN;
+  } else if (sub_log2 < 0) {
     const TileCoord tc = map_tile(blockIdx.x, gridDim.x, tiles_m, tiles_n, group_m, 0);
     m0 = tc.tm * 256;
     n0 = tc.tn * 256;
@@ -515,6 +522,32 @@ hipError_t launch_4w(const GemmArgs& g, hipStream_t st) {
   return hipGetLastError();
 }
 
+// Small M (<= 256 rows): one launch of BM x BN tiles, no 256x256 macro tiles.
+// M <= 64: 64x64 tiles. Otherwise 128x64 if its tiles fit one round of the CUs,
+// else 128x128 (fewer, larger tiles). Measured on MI355X with W read from HBM
+// (M x N, K 5120): 64 x 15360: 64x64 27.8 us vs 29.3 (128x64) and 36.8 (128x128);
+// 256 x 15360: 128x128 40.3 us vs 55.5 (128x64); 256 x 5120: 128x64 29.4 us vs
+// 36.1 (128x128) and 36.0 (64x64). Deeper operand rings (up to 16 stages) and
+// staggered K starts did not change these times.
+constexpr int kSmallMaxM = 256;
+
+template <bool kBf16, bool kGelu, int BM, int BN, int S>
+hipError_t launch_direct(const GemmArgs& g, hipStream_t st) {
+  const int tiles_m = (g.M + BM - 1) / BM, tiles_n = (g.N + BN - 1) / BN;
+  hipLaunchKernelGGL((fp8_gemm_4w<kBf16, kGelu, BM, BN, S>), dim3(tiles_m * tiles_n), dim3(256), 0, st,
+                     (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias,
+                     (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tiles_m, tiles_n, 1, 0, -2);
+  return hipGetLastError();
+}
+
+template <bool kBf16, bool kGelu>
+hipError_t launch_small_m(const GemmArgs& g, hipStream_t st) {
+  if (g.M <= 64) return launch_direct<kBf16, kGelu, 64, 64, 8>(g, st);
+  const int64_t tiles_128x64 = (int64_t)((g.M + 127) / 128) * ((g.N + 63) / 64);
+  if (tiles_128x64 <= device_cus()) return launch_direct<kBf16, kGelu, 128, 64, 6>(g, st);
+  return launch_direct<kBf16, kGelu, 128, 128, 5>(g, st);
+}
+
 template <bool kBf16, bool kGelu>
 hipError_t launch_gemm_t(const GemmArgs& g, hipStream_t st) {
   // main kernel: 64-byte K steps, 16-byte operand rows and scale loads, 8-byte bias
@@ -523,6 +556,7 @@ hipError_t launch_gemm_t(const GemmArgs& g, hipStream_t st) {
                     (g.ldc % 8 == 0) && ((uintptr_t)g.C % 16 == 0) &&
                     ((uintptr_t)g.scales_b % 16 == 0) && ((uintptr_t)g.A % 16 == 0) &&
                     ((uintptr_t)g.W % 16 == 0) && ((uintptr_t)g.bias % 8 == 0);
+  if (fast && g.M <= kSmallMaxM) return launch_small_m<kBf16, kGelu>(g, st);
   if (fast) return launch_4w<kBf16, kGelu>(g, st);
   const int tiles_m = (g.M + 31) / 32, tiles_n = (g.N + 31) / 32;
   const int tiles = tiles_m * tiles_n;
