@@ -206,6 +206,46 @@ def bench_gemm(steps, warmup):
     return res, tot_flops / tot_t / 1e12, ref_agg
 
 
+# The reference's own production GEMM shapes (M, K, N), tuned for gfx950 by
+# deploy/tune_rocm_fp8.py:23-36 (hidden 4096, FFN 16384).
+REFERENCE_TUNED_SHAPES = [(m, k, n) for m in (1024, 1560, 3120)
+                          for k, n in ((4096, 12288), (4096, 4096), (4096, 16384), (16384, 4096))]
+
+
+def bench_reference_shapes(steps, warmup):
+    """This kernel vs the reference's ROCm GEMM (torch._scaled_mm -> hipBLASLt, fp8_linear.py:124-132)
+    on the reference's tuned shapes; each launch reads a different weight copy (as consecutive layers do)."""
+    import torch
+    import joyomni_ops as jo
+    dev = torch.device("cuda:0")
+    out = []
+    for M, K, N in REFERENCE_TUNED_SHAPES:
+        g = torch.Generator().manual_seed(M + K + N)
+        x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
+        w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+        bias = (torch.randn(N, generator=g) * 0.01).to(torch.bfloat16).to(dev)
+        qa = torch.empty(M, K, dtype=torch.float8_e4m3fn, device=dev)
+        sa = torch.empty(M, 1, device=dev)
+        qw = torch.empty(N, K, dtype=torch.float8_e4m3fn, device=dev)
+        sw = torch.empty(N, 1, device=dev)
+        jo.per_token_quant_fp8(x, qa, sa, True)
+        jo.per_token_quant_fp8(w, qw, sw, True)
+        del x, w
+        weights = [qw] + [qw.clone() for _ in range(buffer_sets(N * K) - 1)]
+        swr = sw.reshape(1, N)
+        t = time_launches(Rotation(weights, lambda q: jo.fp8_scaled_mm(qa, q.t(), sa, swr, torch.bfloat16, bias)),
+                          steps, warmup)
+        tr = time_launches(Rotation(weights, lambda q: torch._scaled_mm(
+            qa, q.t(), scale_a=sa, scale_b=swr, bias=bias, out_dtype=torch.bfloat16, use_fast_accum=True)),
+            steps, warmup)
+        flops = 2 * M * N * K
+        out.append({"M": M, "K": K, "N": N, "us": t * 1e6, "tflops": flops / t / 1e12,
+                    "reference_hipblaslt_us": tr * 1e6, "reference_hipblaslt_tflops": flops / tr / 1e12,
+                    "speedup_vs_reference_gpu": tr / t})
+        del weights
+    return out
+
+
 def bench_small_m(steps, warmup):
     """cfg 3: the weights dominate the bytes; each launch reads a different copy of W (as
     consecutive layers do), so W streams from HBM rather than from the MALL."""
@@ -458,7 +498,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time plain launches (no HIP graph)")
     ap.add_argument("--only", default="all",
-                    choices=["all", "qkv", "gemm", "small", "quant", "pack", "norm", "block", "copy"])
+                    choices=["all", "qkv", "gemm", "refgemm", "small", "quant", "pack", "norm", "block", "copy"])
     args = ap.parse_args()
     global EAGER
     EAGER = args.eager
@@ -499,6 +539,13 @@ def main():
         progress(f"cfg2 GEMMs {agg:.0f} TFLOP/s aggregate")
         if "value" not in rec:
             rec.update({"value": round(agg, 1), "unit": "TFLOP/s", "ms_per_step": sum(r["ms"] for r in res)})
+    if args.only in ("all", "refgemm"):
+        rs = bench_reference_shapes(max(5, args.steps // 5), max(2, args.warmup // 2))
+        t_ours = sum(r["us"] for r in rs)
+        t_ref = sum(r["reference_hipblaslt_us"] for r in rs)
+        rec["gemm_reference_shapes"] = {"shapes": rs, "total_us": t_ours, "reference_hipblaslt_total_us": t_ref,
+                                        "speedup_vs_reference_gpu": t_ref / t_ours}
+        progress(f"reference tuned GEMM shapes: {t_ours:.0f} us vs hipBLASLt {t_ref:.0f} us")
     if args.only in ("all", "small"):
         rec["gemm_cfg3_small_m"] = bench_small_m(args.steps, args.warmup)
         progress("cfg3 small-M GEMMs done")

@@ -163,3 +163,34 @@ def test_gelu_epilogue_and_fp16_out(out_dtype):
     got = plain.float().cpu().numpy()
     rms = float(np.sqrt(np.mean(ref32.astype(np.float64) ** 2)))
     assert np.abs(got - ref32).max() <= 2e-2 * rms
+
+
+# The reference's own production GEMM shapes, (M, K, N) as tuned for gfx950 by
+# deploy/tune_rocm_fp8.py:23-36 (hidden 4096, FFN 16384, 1024/1560/3120 tokens).
+REFERENCE_TUNED_SHAPES = [(m, k, n) for m in (1024, 1560, 3120)
+                          for k, n in ((4096, 12288), (4096, 4096), (4096, 16384), (16384, 4096))]
+
+
+@pytest.mark.parametrize("M,K,N", REFERENCE_TUNED_SHAPES)
+def test_reference_tuned_shapes(M, K, N):
+    """Every output checked on 64 sampled rows (rows are independent), cfg-0 distributions."""
+    announce("gemm reference shape", M, K, N)
+    import joyomni_ops as jo
+    g = gen(M + K + N)
+    x = outlier_acts(M, K, g).to(DEV)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    bias = (torch.randn(N, generator=g) * 0.01).to(torch.bfloat16)
+    qa = torch.empty(M, K, dtype=torch.float8_e4m3fn, device=DEV)
+    sa = torch.empty(M, 1, device=DEV)
+    jo.per_token_quant_fp8(x, qa, sa, True)
+    qw_u8, sw = oq.quant_weight_per_channel(u16(w))
+    y = jo.fp8_scaled_mm(qa, to_dev_fp8(qw_u8).t(), sa, torch.from_numpy(sw).to(DEV).reshape(1, -1),
+                         torch.bfloat16, bias.to(DEV))
+    torch.cuda.synchronize()
+    rows = np.sort(np.random.default_rng(2).choice(M, 64, replace=False))
+    rows[-1] = M - 1
+    ri = torch.from_numpy(rows).to(DEV)
+    ys, qa_s = u16(y[ri]), u8(qa[ri])
+    sa_s = sa.cpu().numpy().reshape(-1)[rows]
+    assert_tolerance(ys, og.reference_fp32(qa_s, qw_u8, sa_s, sw, u16(bias)), f"{M}x{K}x{N}")
+    assert_acc_bound(ys, qa_s, qw_u8, sa_s, sw, u16(bias), f"{M}x{K}x{N}")
