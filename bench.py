@@ -185,12 +185,18 @@ def bench_gemm(steps, warmup):
         flops = 2 * M * N * K
         rec = {"shape": name, "M": M, "K": K, "N": N, "ms": t * 1e3,
                "tflops": flops / t / 1e12, "frac_fp8_peak": flops / t / 1e12 / PEAK_FP8_TFLOPS,
-               "epilogue": "bias+gelu_tanh" if name == "ffn_up" else "bias"}
-        # the reference's own ROCm GEMM call (fp8_linear.py:124-132 -> hipBLASLt), same inputs
+               "epilogue": "bias+gelu_tanh" if name == "ffn_up" else "bias",
+               "reference_path": "_scaled_mm + F.gelu" if name == "ffn_up" else "_scaled_mm"}
+        # the reference's own ROCm GEMM call (fp8_linear.py:124-132 -> hipBLASLt), same inputs; for
+        # FFN-up the reference then applies F.gelu(approximate="tanh") as its own kernel (dit.py:87-89)
+        def reference_path():
+            y = torch._scaled_mm(qa, wt, scale_a=sa, scale_b=swr, bias=bias, out_dtype=torch.bfloat16,
+                                 use_fast_accum=True)
+            if name == "ffn_up":
+                y = torch.nn.functional.gelu(y, approximate="tanh")
+            return y
         try:
-            tr = time_launches(lambda: torch._scaled_mm(qa, wt, scale_a=sa, scale_b=swr, bias=bias,
-                                                        out_dtype=torch.bfloat16, use_fast_accum=True),
-                               steps, warmup)
+            tr = time_launches(reference_path, steps, warmup)
             rec["reference_hipblaslt_tflops"] = flops / tr / 1e12
             rec["speedup_vs_reference_gpu"] = tr / t
         except Exception as exc:  # pragma: no cover - depends on the torch build

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define JOY_ABI_VERSION 3
+#define JOY_ABI_VERSION 4
 
 #if defined(__GNUC__) || defined(__clang__)
 #define JOY_API __attribute__((visibility("default")))
@@ -89,6 +89,24 @@ JOY_API joy_status joy_per_token_quant_fp8(const void *input, int input_dtype, v
 JOY_API joy_status joy_fp8_scaled_mm(const void *mat_a, const void *mat_b, const float *scales_a,
                              const float *scales_b, const void *bias, void *out, int out_dtype,
                              int64_t M, int64_t N, int64_t K, int epilogue, void *stream);
+
+/*
+ * FP8 GEMM with the gated residual of the DiT block fused into its epilogue (new
+ * op, no single reference counterpart): the out-projection / FFN-down Fp8Linear
+ * (fp8_linear.py:114-141) followed by fused_add_gate = torch.addcmul(residual, y,
+ * gate) (deploy/xvideo/models/dit/sgl_fused_ops.py:302-305, dit.py:525-528,535-538):
+ *   y        = round(fma(acc[m,n] * scales_b[n], scales_a[m], bias[n]))   as joy_fp8_scaled_mm
+ *   out[m,n] = round(residual[m,n] + y * gate[n])                        (fp32, one rounding)
+ * residual: [M, N] of out_dtype with row stride residual_stride (elements); gate: [N]
+ * of out_dtype. out may be residual itself (in place; then residual_stride == N).
+ * Argument rules otherwise as joy_fp8_scaled_mm.
+ */
+JOY_API joy_status joy_fp8_scaled_mm_gated_residual(const void *mat_a, const void *mat_b,
+                                            const float *scales_a, const float *scales_b,
+                                            const void *bias, const void *residual,
+                                            int64_t residual_stride, const void *gate, void *out,
+                                            int out_dtype, int64_t M, int64_t N, int64_t K,
+                                            void *stream);
 
 /*
  * In-place per-head q/k RMSNorm + interleaved RoPE.

@@ -33,6 +33,54 @@ bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 // The norm/RoPE kernel indexes (token, head) units with 32-bit integers.
 constexpr int64_t kMaxUnits = 0x7ff00000LL;
 
+joy_status scaled_mm_common(const void* mat_a, const void* mat_b, const float* scales_a, const float* scales_b,
+                            const void* bias, void* out, int out_dtype, int64_t M, int64_t N, int64_t K,
+                            int epilogue, const void* residual, int64_t residual_stride, const void* gate,
+                            void* stream) {
+  if (M < 0 || N < 0 || K < 0) return fail(JOY_ERR_INVALID_ARGUMENT, "mat_a and mat_b shapes cannot be multiplied");
+  if (K % 16 != 0)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "mat_a must be multiple of 16 bytes for memory alignment");
+  if (out_dtype != JOY_DTYPE_BF16 && out_dtype != JOY_DTYPE_FP16)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "out_dtype must be Half or BFloat16");
+  if (N % 8 != 0)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "out must be multiple of 16 bytes for memory alignment");
+  if (epilogue != JOY_EPILOGUE_NONE && epilogue != JOY_EPILOGUE_GELU_TANH)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "unknown epilogue %d", epilogue);
+  if (M > 0x7fffffffLL || N > 0x7fffffffLL || K > 0x7fffffffLL)
+    return fail(JOY_ERR_UNSUPPORTED, "dimensions above 2^31-1 are not supported");
+  if (residual && residual_stride < N) return fail(JOY_ERR_INVALID_ARGUMENT, "residual row stride must be >= N");
+  if (residual && !gate) return fail(JOY_ERR_INVALID_ARGUMENT, "gate must be non-null");
+  if (residual && residual == out && residual_stride != N)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "an in-place residual must have row stride N");
+  if (M == 0 || N == 0) return ok();
+  if (!out || !scales_a || !scales_b || (K > 0 && (!mat_a || !mat_b)))
+    return fail(JOY_ERR_INVALID_ARGUMENT, "mat_a, mat_b, scales and out must be non-null");
+  if (!aligned(mat_a, 16) || !aligned(mat_b, 16) || !aligned(out, 16) || !aligned(scales_b, 16))
+    return fail(JOY_ERR_UNSUPPORTED, "mat_a, mat_b, out and scales_b must be 16-byte aligned");
+  if (!aligned(scales_a, 4) || (bias && !aligned(bias, 2)) || (residual && (!aligned(residual, 2) || !aligned(gate, 2))))
+    return fail(JOY_ERR_INVALID_ARGUMENT, "scales_a, bias, residual and gate must be naturally aligned");
+  joy::GemmArgs g;
+  g.A = mat_a;
+  g.W = mat_b;
+  g.scales_a = scales_a;
+  g.scales_b = scales_b;
+  g.bias = bias;
+  g.C = out;
+  g.M = (int)M;
+  g.N = (int)N;
+  g.K = (int)K;
+  g.ldc = N;
+  g.out_bf16 = out_dtype == JOY_DTYPE_BF16;
+  g.gelu = epilogue == JOY_EPILOGUE_GELU_TANH;
+  g.force_generic = (K == 0);
+  g.residual = residual;
+  g.ldr = residual_stride;
+  g.gate = gate;
+  return hip_status(joy::launch_fp8_gemm(g, (hipStream_t)stream),
+                    residual ? "fp8_scaled_mm_gated_residual launch" : "fp8_scaled_mm launch");
+}
+
+
 }  // namespace
 
 extern "C" {
@@ -60,42 +108,21 @@ joy_status joy_per_token_quant_fp8(const void* input, int input_dtype, void* out
                     "per_token_quant_fp8 launch");
 }
 
+
 joy_status joy_fp8_scaled_mm(const void* mat_a, const void* mat_b, const float* scales_a,
                              const float* scales_b, const void* bias, void* out, int out_dtype,
                              int64_t M, int64_t N, int64_t K, int epilogue, void* stream) {
-  if (M < 0 || N < 0 || K < 0) return fail(JOY_ERR_INVALID_ARGUMENT, "mat_a and mat_b shapes cannot be multiplied");
-  if (K % 16 != 0)
-    return fail(JOY_ERR_INVALID_ARGUMENT, "mat_a must be multiple of 16 bytes for memory alignment");
-  if (out_dtype != JOY_DTYPE_BF16 && out_dtype != JOY_DTYPE_FP16)
-    return fail(JOY_ERR_INVALID_ARGUMENT, "out_dtype must be Half or BFloat16");
-  if (N % 8 != 0)
-    return fail(JOY_ERR_INVALID_ARGUMENT, "out must be multiple of 16 bytes for memory alignment");
-  if (epilogue != JOY_EPILOGUE_NONE && epilogue != JOY_EPILOGUE_GELU_TANH)
-    return fail(JOY_ERR_INVALID_ARGUMENT, "unknown epilogue %d", epilogue);
-  if (M > 0x7fffffffLL || N > 0x7fffffffLL || K > 0x7fffffffLL)
-    return fail(JOY_ERR_UNSUPPORTED, "dimensions above 2^31-1 are not supported");
-  if (M == 0 || N == 0) return ok();
-  if (!out || !scales_a || !scales_b || (K > 0 && (!mat_a || !mat_b)))
-    return fail(JOY_ERR_INVALID_ARGUMENT, "mat_a, mat_b, scales and out must be non-null");
-  if (!aligned(mat_a, 16) || !aligned(mat_b, 16) || !aligned(out, 16) || !aligned(scales_b, 16))
-    return fail(JOY_ERR_UNSUPPORTED, "mat_a, mat_b, out and scales_b must be 16-byte aligned");
-  if (!aligned(scales_a, 4) || (bias && !aligned(bias, 2)))
-    return fail(JOY_ERR_INVALID_ARGUMENT, "scales_a and bias must be naturally aligned");
-  joy::GemmArgs g;
-  g.A = mat_a;
-  g.W = mat_b;
-  g.scales_a = scales_a;
-  g.scales_b = scales_b;
-  g.bias = bias;
-  g.C = out;
-  g.M = (int)M;
-  g.N = (int)N;
-  g.K = (int)K;
-  g.ldc = N;
-  g.out_bf16 = out_dtype == JOY_DTYPE_BF16;
-  g.gelu = epilogue == JOY_EPILOGUE_GELU_TANH;
-  g.force_generic = (K == 0);
-  return hip_status(joy::launch_fp8_gemm(g, (hipStream_t)stream), "fp8_scaled_mm launch");
+  return scaled_mm_common(mat_a, mat_b, scales_a, scales_b, bias, out, out_dtype, M, N, K, epilogue, nullptr, 0,
+                          nullptr, stream);
+}
+
+joy_status joy_fp8_scaled_mm_gated_residual(const void* mat_a, const void* mat_b, const float* scales_a,
+                                            const float* scales_b, const void* bias, const void* residual,
+                                            int64_t residual_stride, const void* gate, void* out, int out_dtype,
+                                            int64_t M, int64_t N, int64_t K, void* stream) {
+  if (!residual) return fail(JOY_ERR_INVALID_ARGUMENT, "residual must be non-null");
+  return scaled_mm_common(mat_a, mat_b, scales_a, scales_b, bias, out, out_dtype, M, N, K, JOY_EPILOGUE_NONE,
+                          residual, residual_stride, gate, stream);
 }
 
 joy_status joy_fused_qk_norm_rope_3d_paired(void* q, void* k, int64_t batch, int64_t seq_len,

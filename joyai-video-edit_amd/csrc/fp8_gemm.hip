@@ -8,6 +8,9 @@
 // dtype); epilogue order of fp8_gemm.cu:99-136. Optional GELU-tanh epilogue
 // applies F.gelu(approximate="tanh") to the rounded output, as the reference
 // model does after its up-projection (deploy/xvideo/models/dit/dit.py:87-89).
+// Optional gated-residual epilogue: out = round(residual[m, n] + round(gemm) * gate[n]),
+// the reference block's projection + fused_add_gate pair (dit.py:525-528, 535-538;
+// sgl_fused_ops.py:302-305); residual and output may be the same buffer.
 //
 // Main kernel (fp8_gemm_4w, any M, N with K % 64 == 0):
 //  * 256 threads = 4 waves in 2x2, one wave per SIMD; macro tile 256x256 for the
@@ -54,16 +57,12 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-
-// Two fp32 -> packed 16-bit pair, round to nearest even (v_cvt_pk_bf16_f32 on gfx950).
+// Two fp32 -> packed 16-bit pair, round to nearest even (v_cvt_pk_bf16_f32 /
+// v_cvt_pk_f16_f32 on gfx950).
 template <bool kBf16>
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  const f32x2_t v = {lo, hi};
-  if constexpr (kBf16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_t));
+  if constexpr (kBf16) return pack_bf16x2(lo, hi);
+  return pack_fp16x2(lo, hi);
 }
 
 // Value of a packed 16-bit pair element (exact).
@@ -102,16 +101,35 @@ __device__ __forceinline__ void load_col_operands(ColOperands<FN>& c, int n_base
     }
 }
 
+// Optional gated residual of the epilogue (fused_add_gate, sgl_fused_ops.py:302-305):
+// out = round(residual + round(gemm) * gate[n]) -- the GEMM output is rounded first,
+// as the reference rounds the projection before torch.addcmul.
+struct ResidualArgs {
+  const uint16_t* ptr;
+  int64_t ld;
+  const uint16_t* gate;
+};
+
+// Epilogue kinds, a template parameter so that the plain and GELU kernels carry no
+// residual registers.
+enum Epi : int { kEpiPlain = 0, kEpiGelu = 1, kEpiResidual = 2 };
+
+template <bool kBf16>
+__device__ __forceinline__ uint32_t gated_pair(uint32_t y, uint32_t x, uint32_t g) {
+  return pack2<kBf16>(__builtin_fmaf(unpack_lo<kBf16>(y), unpack_lo<kBf16>(g), unpack_lo<kBf16>(x)),
+                      __builtin_fmaf(unpack_hi<kBf16>(y), unpack_hi<kBf16>(g), unpack_hi<kBf16>(x)));
+}
+
 // Epilogue through LDS: the wave's (32*FN) x (32*FM) tile is rounded to 16-bit, written
 // to a private LDS staging area [32*FM rows][32*FN columns] with a row pitch of
 // 32*FN*2 + 16 bytes (16 lanes x 16 bytes cover all banks once for the 8-byte writes
 // and for the 16-byte reads), then read back row-wise so that each global store
 // instruction writes 64 x 16 contiguous bytes (whole row segments).
-template <bool kBf16, bool kGelu, int FN, int FM>
+template <bool kBf16, int kEpi, int FN, int FM>
 __device__ __forceinline__ void store_tile_lds(const v16f (&acc)[FN][FM], const ColOperands<FN>& col,
                                                const float (&sav)[FM], uint8_t* stage, int m_base,
                                                int n_base, int lane, uint16_t* __restrict__ C,
-                                               int M, int N, int64_t ldc) {
+                                               int M, int N, int64_t ldc, const ResidualArgs& res) {
   constexpr int ROW_BYTES = 32 * FN * 2;
   constexpr int PITCH = ROW_BYTES + 16;
   const int frow = lane & 31, g = lane >> 5;
@@ -131,7 +149,7 @@ __device__ __forceinline__ void store_tile_lds(const v16f (&acc)[FN][FM], const 
 #pragma unroll
         for (int e = 0; e < 4; ++e) o[e] = __builtin_fmaf(acc[i][j][q * 4 + e] * sbe[e], sav[j], be[e]);
         uint2 pk = make_uint2(pack2<kBf16>(o[0], o[1]), pack2<kBf16>(o[2], o[3]));
-        if constexpr (kGelu) {
+        if constexpr (kEpi == kEpiGelu) {
           // the reference applies GELU to the rounded GEMM output and rounds again
           pk = make_uint2(pack2<kBf16>(gelu_tanh(unpack_lo<kBf16>(pk.x)), gelu_tanh(unpack_hi<kBf16>(pk.x))),
                           pack2<kBf16>(gelu_tanh(unpack_lo<kBf16>(pk.y)), gelu_tanh(unpack_hi<kBf16>(pk.y))));
@@ -144,19 +162,29 @@ __device__ __forceinline__ void store_tile_lds(const v16f (&acc)[FN][FM], const 
   constexpr int RPI = 64 / CPL;
   const int rr = lane / CPL, cc = lane % CPL;
   const int n = n_base + cc * 8;
+  uint4 gv = make_uint4(0, 0, 0, 0);
+  if constexpr (kEpi == kEpiResidual)
+    if (n < N) gv = *(const uint4*)(res.gate + n);
 #pragma unroll
   for (int r0 = 0; r0 < 32 * FM; r0 += RPI) {
     const int r = r0 + rr;
-    const uint4 v = *(const uint4*)(stage + r * PITCH + cc * 16);
+    uint4 v = *(const uint4*)(stage + r * PITCH + cc * 16);
     const int m = m_base + r;
-    if (m < M && n < N) *(uint4*)(C + (int64_t)m * ldc + n) = v;
+    if (m < M && n < N) {
+      if constexpr (kEpi == kEpiResidual) {
+        const uint4 x = *(const uint4*)(res.ptr + (int64_t)m * res.ld + n);
+        v = make_uint4(gated_pair<kBf16>(v.x, x.x, gv.x), gated_pair<kBf16>(v.y, x.y, gv.y),
+                       gated_pair<kBf16>(v.z, x.z, gv.z), gated_pair<kBf16>(v.w, x.w, gv.w));
+      }
+      *(uint4*)(C + (int64_t)m * ldc + n) = v;
+    }
   }
 }
 
 template <bool kBf16>
 __device__ __forceinline__ float round_out(float v) {
   if constexpr (kBf16) return __uint_as_float(f32_to_bf16_bits(v) << 16);
-  return (float)(_Float16)v;
+  return round_fp16(v);
 }
 
 template <bool kBf16>
@@ -216,11 +244,11 @@ __device__ __forceinline__ void block_barrier() {
 
 // Generic fallback for any M, N, K with K % 16 == 0: one wave computes a 32x32
 // output tile straight from global memory (no LDS), zero-padding K to 64.
-template <bool kBf16, bool kGelu>
+template <bool kBf16, int kEpi>
 __global__ __launch_bounds__(256) void fp8_gemm_generic(
     const uint8_t* __restrict__ A, const uint8_t* __restrict__ W, const float* __restrict__ sa,
     const float* __restrict__ sb, const uint16_t* __restrict__ bias, uint16_t* __restrict__ C,
-    int M, int N, int K, int64_t ldc, int tiles_n) {
+    int M, int N, int K, int64_t ldc, int tiles_n, ResidualArgs res) {
   const int lane = threadIdx.x & 63;
   const int tile = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int tm = tile / tiles_n, tn = tile % tiles_n;
@@ -262,12 +290,15 @@ __global__ __launch_bounds__(256) void fp8_gemm_generic(
     const int n = n0 + (r >> 2) * 8 + g * 4 + (r & 3);
     if (n >= N) continue;
     float v = round_out<kBf16>(__builtin_fmaf(acc[r] * sb[n], s_a, bias_value<kBf16>(bias, n)));
-    if constexpr (kGelu) v = round_out<kBf16>(gelu_tanh(v));
+    if constexpr (kEpi == kEpiGelu) v = round_out<kBf16>(gelu_tanh(v));
+    if constexpr (kEpi == kEpiResidual)
+      v = round_out<kBf16>(__builtin_fmaf(v, bias_value<kBf16>(res.gate, n),
+                                          bias_value<kBf16>(res.ptr, (int64_t)m * res.ld + n)));
     uint16_t bits;
     if constexpr (kBf16) {
       bits = (uint16_t)f32_to_bf16_bits(v);
     } else {
-      bits = __builtin_bit_cast(uint16_t, (_Float16)v);
+      bits = (uint16_t)f32_to_fp16_bits(v);
     }
     C[(int64_t)m * ldc + n] = bits;
   }
@@ -312,12 +343,12 @@ __device__ __forceinline__ void sched_pattern() {
 // M fastest within each XCD's contiguous range (the M tiles of one weight tile
 // run together, so W is fetched once per XCD).
 // ---------------------------------------------------------------------------
-template <bool kBf16, bool kGelu, int BM, int BN, int S>
+template <bool kBf16, int kEpi, int BM, int BN, int S>
 __global__ __launch_bounds__(256, 1) void fp8_gemm_4w(
     const uint8_t* __restrict__ A, const uint8_t* __restrict__ W, const float* __restrict__ sa,
     const float* __restrict__ sb, const uint16_t* __restrict__ bias, uint16_t* __restrict__ C,
     int M, int N, int K, int64_t ldc, int tiles_m, int tiles_n, int group_m, int tile_base,
-    int sub_log2) {
+    int sub_log2, ResidualArgs res) {
   constexpr int KS = 64, NW = 4;
   constexpr int WTM = BM / 2, WTN = BN / 2;  // wave sub-tile
   constexpr int FM = WTM / 32, FN = WTN / 32;
@@ -463,8 +494,12 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4w(
   wait_vmcnt<0>();
   __builtin_amdgcn_s_waitcnt(0x0070);
   block_barrier();
-  store_tile_lds<kBf16, kGelu, FN, FM>(acc, col, sav, lds + wave * STAGE_BYTES, m0 + wm * WTM,
-                                       n0 + wn * WTN, lane, C, M, N, ldc);
+  store_tile_lds<kBf16, kEpi, FN, FM>(acc, col, sav, lds + wave * STAGE_BYTES, m0 + wm * WTM,
+                                       n0 + wn * WTN, lane, C, M, N, ldc, res);
+}
+
+ResidualArgs residual_args(const GemmArgs& g) {
+  return ResidualArgs{(const uint16_t*)g.residual, g.ldr, (const uint16_t*)g.gate};
 }
 
 // Number of compute units of the current device (cached per device).
@@ -485,7 +520,7 @@ int device_cus() {
 // the last, partial round split into 4 (128x128) or 2 (256x128) sub-tiles so that
 // more CUs share that round. Both launches go to the same stream; the result does
 // not depend on the split (every output element sums its K products in the same order).
-template <bool kBf16, bool kGelu>
+template <bool kBf16, int kEpi>
 hipError_t launch_4w(const GemmArgs& g, hipStream_t st) {
   constexpr int S = 5;
   const int tiles_m = (g.M + 255) / 256, tiles_n = (g.N + 255) / 256;
@@ -501,22 +536,22 @@ hipError_t launch_4w(const GemmArgs& g, hipStream_t st) {
   }
   const int bulk = T - rem;
   if (bulk > 0) {
-    hipLaunchKernelGGL((fp8_gemm_4w<kBf16, kGelu, 256, 256, S>), dim3(bulk), dim3(256), 0, st,
+    hipLaunchKernelGGL((fp8_gemm_4w<kBf16, kEpi, 256, 256, S>), dim3(bulk), dim3(256), 0, st,
                        (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a, g.scales_b,
                        (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tiles_m, tiles_n,
-                       kGroupM, 0, -1);
+                       kGroupM, 0, -1, residual_args(g));
   }
   if (rem > 0) {
     if (sub_log2 == 2) {
-      hipLaunchKernelGGL((fp8_gemm_4w<kBf16, kGelu, 128, 128, S>), dim3(rem << 2), dim3(256), 0, st,
+      hipLaunchKernelGGL((fp8_gemm_4w<kBf16, kEpi, 128, 128, S>), dim3(rem << 2), dim3(256), 0, st,
                          (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a, g.scales_b,
                          (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tiles_m,
-                         tiles_n, kGroupM, bulk, 2);
+                         tiles_n, kGroupM, bulk, 2, residual_args(g));
     } else {
-      hipLaunchKernelGGL((fp8_gemm_4w<kBf16, kGelu, 256, 128, S>), dim3(rem << 1), dim3(256), 0, st,
+      hipLaunchKernelGGL((fp8_gemm_4w<kBf16, kEpi, 256, 128, S>), dim3(rem << 1), dim3(256), 0, st,
                          (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a, g.scales_b,
                          (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tiles_m,
-                         tiles_n, kGroupM, bulk, 1);
+                         tiles_n, kGroupM, bulk, 1, residual_args(g));
     }
   }
   return hipGetLastError();
@@ -531,38 +566,40 @@ hipError_t launch_4w(const GemmArgs& g, hipStream_t st) {
 // staggered K starts did not change these times.
 constexpr int kSmallMaxM = 256;
 
-template <bool kBf16, bool kGelu, int BM, int BN, int S>
+template <bool kBf16, int kEpi, int BM, int BN, int S>
 hipError_t launch_direct(const GemmArgs& g, hipStream_t st) {
   const int tiles_m = (g.M + BM - 1) / BM, tiles_n = (g.N + BN - 1) / BN;
-  hipLaunchKernelGGL((fp8_gemm_4w<kBf16, kGelu, BM, BN, S>), dim3(tiles_m * tiles_n), dim3(256), 0, st,
+  hipLaunchKernelGGL((fp8_gemm_4w<kBf16, kEpi, BM, BN, S>), dim3(tiles_m * tiles_n), dim3(256), 0, st,
                      (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias,
-                     (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tiles_m, tiles_n, 1, 0, -2);
+                     (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tiles_m, tiles_n, 1, 0, -2, residual_args(g));
   return hipGetLastError();
 }
 
-template <bool kBf16, bool kGelu>
+template <bool kBf16, int kEpi>
 hipError_t launch_small_m(const GemmArgs& g, hipStream_t st) {
-  if (g.M <= 64) return launch_direct<kBf16, kGelu, 64, 64, 8>(g, st);
+  if (g.M <= 64) return launch_direct<kBf16, kEpi, 64, 64, 8>(g, st);
   const int64_t tiles_128x64 = (int64_t)((g.M + 127) / 128) * ((g.N + 63) / 64);
-  if (tiles_128x64 <= device_cus()) return launch_direct<kBf16, kGelu, 128, 64, 6>(g, st);
-  return launch_direct<kBf16, kGelu, 128, 128, 5>(g, st);
+  if (tiles_128x64 <= device_cus()) return launch_direct<kBf16, kEpi, 128, 64, 6>(g, st);
+  return launch_direct<kBf16, kEpi, 128, 128, 5>(g, st);
 }
 
-template <bool kBf16, bool kGelu>
+template <bool kBf16, int kEpi>
 hipError_t launch_gemm_t(const GemmArgs& g, hipStream_t st) {
   // main kernel: 64-byte K steps, 16-byte operand rows and scale loads, 8-byte bias
   // loads, 16-byte output row segments
   const bool fast = !g.force_generic && g.K >= 64 && (g.K % 64 == 0) && (g.N % 8 == 0) &&
                     (g.ldc % 8 == 0) && ((uintptr_t)g.C % 16 == 0) &&
                     ((uintptr_t)g.scales_b % 16 == 0) && ((uintptr_t)g.A % 16 == 0) &&
-                    ((uintptr_t)g.W % 16 == 0) && ((uintptr_t)g.bias % 8 == 0);
-  if (fast && g.M <= kSmallMaxM) return launch_small_m<kBf16, kGelu>(g, st);
-  if (fast) return launch_4w<kBf16, kGelu>(g, st);
+                    ((uintptr_t)g.W % 16 == 0) && ((uintptr_t)g.bias % 8 == 0) &&
+                    (!g.residual || ((uintptr_t)g.residual % 16 == 0 && g.ldr % 8 == 0 &&
+                                     (uintptr_t)g.gate % 16 == 0));
+  if (fast && g.M <= kSmallMaxM) return launch_small_m<kBf16, kEpi>(g, st);
+  if (fast) return launch_4w<kBf16, kEpi>(g, st);
   const int tiles_m = (g.M + 31) / 32, tiles_n = (g.N + 31) / 32;
   const int tiles = tiles_m * tiles_n;
-  hipLaunchKernelGGL((fp8_gemm_generic<kBf16, kGelu>), dim3((tiles + 3) / 4), dim3(256), 0, st,
+  hipLaunchKernelGGL((fp8_gemm_generic<kBf16, kEpi>), dim3((tiles + 3) / 4), dim3(256), 0, st,
                      (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a, g.scales_b,
-                     (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tiles_n);
+                     (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tiles_n, residual_args(g));
   return hipGetLastError();
 }
 
@@ -570,10 +607,13 @@ hipError_t launch_gemm_t(const GemmArgs& g, hipStream_t st) {
 
 hipError_t launch_fp8_gemm(const GemmArgs& g, hipStream_t st) {
   if (g.M == 0 || g.N == 0) return hipSuccess;
+  if (g.residual && g.gelu) return hipErrorInvalidValue;
   if (g.out_bf16) {
-    return g.gelu ? launch_gemm_t<true, true>(g, st) : launch_gemm_t<true, false>(g, st);
+    if (g.residual) return launch_gemm_t<true, kEpiResidual>(g, st);
+    return g.gelu ? launch_gemm_t<true, kEpiGelu>(g, st) : launch_gemm_t<true, kEpiPlain>(g, st);
   }
-  return g.gelu ? launch_gemm_t<false, true>(g, st) : launch_gemm_t<false, false>(g, st);
+  if (g.residual) return launch_gemm_t<false, kEpiResidual>(g, st);
+  return g.gelu ? launch_gemm_t<false, kEpiGelu>(g, st) : launch_gemm_t<false, kEpiPlain>(g, st);
 }
 
 }  // namespace joy

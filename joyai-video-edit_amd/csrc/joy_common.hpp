@@ -37,16 +37,56 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_vt));
 }
 
-// fp16 bits -> fp32 (exact).
-__device__ __forceinline__ float fp16_bits_to_f32(uint32_t h) {
-  _Float16 v = __builtin_bit_cast(_Float16, (uint16_t)h);
-  return (float)v;
+// Value barrier around fp16 conversions (an empty asm: no instruction). Without it
+// the compiler folds fma + fp32 -> fp16 rounding into one v_fma_mixlo_f16, a single
+// rounding of the exact result where the reference's fp32 arithmetic rounds twice
+// (to fp32, then to fp16), and folds fp16 -> fp32 conversions into mixed-precision
+// FMA sources. Pinning the fp32 value keeps v_cvt_f32_f16 / v_cvt_pk_f16_f32 and
+// plain fp32 arithmetic, so fp16 results follow the fp32 formula bit for bit.
+__device__ __forceinline__ float pin_f32(float v) {
+  __asm__("" : "+v"(v));
+  return v;
 }
 
+// fp16 bits -> fp32 (exact, denormals kept).
+__device__ __forceinline__ float fp16_bits_to_f32(uint32_t h) {
+  const _Float16 v = __builtin_bit_cast(_Float16, (uint16_t)h);
+  return pin_f32((float)v);
+}
+
+// fp16 bits of a finite value -> fp32 (exact, denormals kept), without a conversion
+// instruction: the 15 magnitude bits placed at the fp32 exponent/mantissa position
+// read as x * 2^-112 (an fp32 denormal for fp16 denormals), and one exact multiply
+// by 2^112 restores x. For rows known to be finite; inf / NaN bits give large finite
+// values.
+__device__ __forceinline__ float fp16_finite_bits_to_f32(uint32_t h) {
+  const float scaled = __uint_as_float(((h & 0x7fffu) << 13) | ((h & 0x8000u) << 16));
+  return scaled * 0x1p112f;
+}
+
+// fp16 bits -> fp32, exact for every value (inf / NaN bits rebuilt with the fp32
+// exponent), without a conversion instruction.
+__device__ __forceinline__ float fp16_bits_to_f32_arith(uint32_t h) {
+  const uint32_t special = ((h & 0x7fffu) << 13) | 0x7f800000u | ((h & 0x8000u) << 16);
+  return (h & 0x7c00u) == 0x7c00u ? __uint_as_float(special) : fp16_finite_bits_to_f32(h);
+}
+
+// fp32 -> fp16 bits, round to nearest even, from the fp32 value.
+__device__ __forceinline__ uint32_t f32_to_fp16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)pin_f32(f));
+}
+
+// fp32 -> fp16 -> fp32 (the value an fp16 store keeps).
+__device__ __forceinline__ float round_fp16(float f) {
+  return fp16_bits_to_f32(f32_to_fp16_bits(f));
+}
+
+typedef _Float16 f16x2_vt __attribute__((ext_vector_type(2)));
+
+// Two fp32 -> packed fp16 pair, round to nearest even (v_cvt_pk_f16_f32 on gfx950).
 __device__ __forceinline__ uint32_t pack_fp16x2(float lo, float hi) {
-  uint16_t a = __builtin_bit_cast(uint16_t, (_Float16)lo);
-  uint16_t b = __builtin_bit_cast(uint16_t, (_Float16)hi);
-  return (uint32_t)a | ((uint32_t)b << 16);
+  const f32x2_vt v = {pin_f32(lo), pin_f32(hi)};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_vt));
 }
 
 // Four fp32 values -> four e4m3fn bytes packed little-endian (RNE).

@@ -42,6 +42,10 @@ struct GemmArgs {
   bool out_bf16;
   bool gelu;
   bool force_generic;
+  // gated residual epilogue: C = round(residual + round(gemm) * gate[n]) when residual != null
+  const void* residual;  // [M, N] of out dtype, row stride ldr (may equal C with ldr == ldc)
+  int64_t ldr;
+  const void* gate;  // [N] of out dtype
 };
 
 // bf16 [len, H, D] view: element (t, h, d) at ptr[t * stride_token + h * stride_head + d].

@@ -37,14 +37,14 @@ __device__ __forceinline__ float load_elem(const void* p, int64_t i) {
 template <int DT>
 __device__ __forceinline__ float round_elem(float v) {
   if constexpr (DT == 0) return __uint_as_float(f32_to_bf16_bits(v) << 16);
-  if constexpr (DT == 1) return (float)(_Float16)v;
+  if constexpr (DT == 1) return round_fp16(v);
   return v;
 }
 
 template <int DT>
 __device__ __forceinline__ void store_elem(void* p, int64_t i, float v) {
   if constexpr (DT == 0) ((uint16_t*)p)[i] = (uint16_t)f32_to_bf16_bits(v);
-  if constexpr (DT == 1) ((uint16_t*)p)[i] = __builtin_bit_cast(uint16_t, (_Float16)v);
+  if constexpr (DT == 1) ((uint16_t*)p)[i] = (uint16_t)f32_to_fp16_bits(v);
   if constexpr (DT == 2) ((float*)p)[i] = v;
 }
 
@@ -444,7 +444,7 @@ __global__ __launch_bounds__(256) void norm_mod_scalar(NormModArgs a) {
     const float y = y_at(k);
     if (a.out) store_elem<DT>(a.out, row * a.N + k, y);
     if constexpr (kFp8) {
-      const uint32_t bits = DT == 1 ? (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)y)
+      const uint32_t bits = DT == 1 ? f32_to_fp16_bits(y)
                                     : (__float_as_uint(y) >> 16);
       const uint32_t m = bits & 0x7fffu;
       amax = m > amax ? m : amax;

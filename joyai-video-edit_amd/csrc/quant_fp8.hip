@@ -27,14 +27,21 @@ __device__ __forceinline__ float half_to_f32(uint32_t bits16) {
   return __uint_as_float(bits16 << 16);
 }
 
-template <bool kFp16>
+// fp16 values are converted arithmetically (exact, denormals kept; kFinite: every
+// value of the row is finite, so inf / NaN need no select): plain fp32 arithmetic
+// on the converted values, with no register barrier that would make the widest rows
+// spill.
+template <bool kFp16, bool kFinite>
 __device__ __forceinline__ void unpack8(const uint4& v, float f[8]) {
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    if constexpr (kFp16) {
-      f[2 * i] = fp16_bits_to_f32(w[i] & 0xffffu);
-      f[2 * i + 1] = fp16_bits_to_f32(w[i] >> 16);
+    if constexpr (kFp16 && kFinite) {
+      f[2 * i] = fp16_finite_bits_to_f32(w[i] & 0xffffu);
+      f[2 * i + 1] = fp16_finite_bits_to_f32(w[i] >> 16);
+    } else if constexpr (kFp16) {
+      f[2 * i] = fp16_bits_to_f32_arith(w[i] & 0xffffu);
+      f[2 * i + 1] = fp16_bits_to_f32_arith(w[i] >> 16);
     } else {
       f[2 * i] = bf16_lo(w[i]);
       f[2 * i + 1] = bf16_hi(w[i]);
@@ -139,7 +146,7 @@ __global__ __launch_bounds__(256) void quant_rows_vec(const uint4* __restrict__ 
       const int idx = lane + i * kWave;
       if (idx < nvec) {
         float f[8];
-        unpack8<kFp16>(v[i], f);
+        unpack8<kFp16, true>(v[i], f);
 #pragma unroll
         for (int j = 0; j < 8; ++j)
           f[j] = __builtin_amdgcn_fmed3f(scale_value<kDivide>(f[j], s, r), -kFp8Max, kFp8Max);
@@ -150,23 +157,22 @@ __global__ __launch_bounds__(256) void quant_rows_vec(const uint4* __restrict__ 
       }
     }
   } else {
+    // rows holding inf / NaN (cold): read the row again rather than index v[] from a
+    // rolled loop, so that v[] stays in registers
+#pragma unroll 1
+    for (int idx = lane; idx < nvec; idx += kWave) {
+      float f[8];
+      unpack8<kFp16, false>(src[idx], f);
+      uint32_t b[8];
 #pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-      const int idx = lane + i * kWave;
-      if (idx < nvec) {
-        float f[8];
-        unpack8<kFp16>(v[i], f);
-        uint32_t b[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          float t = kDivide ? f[j] / s : f[j] * r;
-          b[j] = f32_to_e4m3fn_soft(clamp_fp8(t));
-        }
-        uint2 o;
-        o.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
-        o.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
-        dst[idx] = o;
+      for (int j = 0; j < 8; ++j) {
+        float t = kDivide ? f[j] / s : f[j] * r;
+        b[j] = f32_to_e4m3fn_soft(clamp_fp8(t));
       }
+      uint2 o;
+      o.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+      o.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+      dst[idx] = o;
     }
   }
 }

@@ -43,6 +43,7 @@ __all__ = [
     "fp8_scaled_mm_gelu_tanh",
     "fused_qkv_norm_rope_cache",
     "fused_norm_scale_shift_fp8",
+    "fp8_scaled_mm_gated_residual",
 ]
 
 _NS = "joyomni_ops"
@@ -74,6 +75,12 @@ _lib_def.define(
 _lib_def.define(
     "fp8_scaled_mm_gelu_tanh(Tensor mat_a, Tensor mat_b, Tensor scales_a, Tensor scales_b, "
     "ScalarType out_dtype, Tensor? bias) -> Tensor")
+_lib_def.define(
+    "fp8_scaled_mm_gated_residual(Tensor mat_a, Tensor mat_b, Tensor scales_a, Tensor scales_b, "
+    "Tensor residual, Tensor gate, Tensor? bias) -> Tensor")
+_lib_def.define(
+    "fp8_scaled_mm_gated_residual_(Tensor mat_a, Tensor mat_b, Tensor scales_a, Tensor scales_b, "
+    "Tensor(a!) residual, Tensor gate, Tensor? bias) -> ()")
 _lib_def.define(
     "fused_norm_scale_shift_fp8(Tensor x, Tensor? gamma_opt, Tensor? beta_opt, Tensor scale, "
     "Tensor shift, int norm_type, float eps, Tensor(a!) output_q, Tensor(b!) output_s, "
@@ -150,7 +157,7 @@ def _per_token_quant_fp8_cuda(input, output_q, output_s, exact_division):
 # --------------------------------------------------------------------------
 # GEMM
 # --------------------------------------------------------------------------
-def _scaled_mm_impl(mat_a, mat_b, scales_a, scales_b, out_dtype, bias, epilogue):
+def _scaled_mm_checks(mat_a, mat_b, scales_a, scales_b, out_dtype, bias):
     # checks of fp8_gemm.cu:1457-1487
     _check(mat_a.is_cuda, "mat_a must be a CUDA tensor")
     _check(mat_b.is_cuda, "mat_b must be a CUDA tensor")
@@ -181,9 +188,14 @@ def _scaled_mm_impl(mat_a, mat_b, scales_a, scales_b, out_dtype, bias, epilogue)
     # Row stride of A and column stride of B must be K (dense rows).
     _check(M <= 1 or mat_a.stride(0) == K, "mat_a rows must be dense (stride(0) == K)")
     _check(N <= 1 or mat_b.stride(1) == K, "mat_b columns must be dense (stride(1) == K)")
-    out = torch.empty((M, N), device=mat_a.device, dtype=out_dtype)
-    _check((out.size(1) * out.element_size()) % 16 == 0,
+    _check((N * torch.empty((), dtype=out_dtype).element_size()) % 16 == 0,
            "out must be multiple of 16 bytes for memory alignment")
+    return M, N, K
+
+
+def _scaled_mm_impl(mat_a, mat_b, scales_a, scales_b, out_dtype, bias, epilogue):
+    M, N, K = _scaled_mm_checks(mat_a, mat_b, scales_a, scales_b, out_dtype, bias)
+    out = torch.empty((M, N), device=mat_a.device, dtype=out_dtype)
     with torch.cuda.device(mat_a.device):
         st = _LIB.joy_fp8_scaled_mm(
             _ptr(mat_a), _ptr(mat_b), _ptr(scales_a), _ptr(scales_b), _ptr(bias), _ptr(out),
@@ -201,6 +213,40 @@ def _fp8_scaled_mm_cuda(mat_a, mat_b, scales_a, scales_b, out_dtype, bias=None):
 def _fp8_scaled_mm_gelu_cuda(mat_a, mat_b, scales_a, scales_b, out_dtype, bias=None):
     return _scaled_mm_impl(mat_a, mat_b, scales_a, scales_b, out_dtype, bias,
                            _lib.JOY_EPILOGUE_GELU_TANH)
+
+
+def _gated_residual_impl(mat_a, mat_b, scales_a, scales_b, residual, gate, bias, out):
+    """out = residual + fp8_scaled_mm(...) * gate (fused_add_gate, sgl_fused_ops.py:302-305)."""
+    out_dtype = residual.dtype
+    _check(out_dtype in (torch.float16, torch.bfloat16), "residual must be Half or BFloat16")
+    M, N, K = _scaled_mm_checks(mat_a, mat_b, scales_a, scales_b, out_dtype, bias)
+    _check(residual.is_cuda and gate.is_cuda, "residual and gate must be CUDA tensors")
+    _check(residual.dim() == 2 and tuple(residual.shape) == (M, N), "residual must be [M, N]")
+    _check(residual.stride(1) == 1 or N <= 1, "residual rows must be contiguous")
+    _check(gate.numel() == N, "size of gate is not matched")
+    _check(gate.dtype == out_dtype, "gate dtype must match residual dtype")
+    gate = gate.reshape(N)
+    if gate.stride(0) != 1 or gate.data_ptr() % 16:
+        gate = gate.clone(memory_format=torch.contiguous_format)  # N values: a 16-byte aligned copy
+    ld = residual.stride(0) if M > 1 else N
+    with torch.cuda.device(mat_a.device):
+        st = _LIB.joy_fp8_scaled_mm_gated_residual(
+            _ptr(mat_a), _ptr(mat_b), _ptr(scales_a), _ptr(scales_b), _ptr(bias), _ptr(residual), ld,
+            _ptr(gate), _ptr(out), _OUT_CODE[out_dtype], M, N, K, _stream(mat_a))
+    _lib.check(_LIB, st)
+
+
+@torch.library.impl(_lib_def, "fp8_scaled_mm_gated_residual", "CUDA")
+def _fp8_scaled_mm_gated_residual_cuda(mat_a, mat_b, scales_a, scales_b, residual, gate, bias=None):
+    out = torch.empty(residual.shape, device=residual.device, dtype=residual.dtype)
+    _gated_residual_impl(mat_a, mat_b, scales_a, scales_b, residual, gate, bias, out)
+    return out
+
+
+@torch.library.impl(_lib_def, "fp8_scaled_mm_gated_residual_", "CUDA")
+def _fp8_scaled_mm_gated_residual_inplace_cuda(mat_a, mat_b, scales_a, scales_b, residual, gate, bias=None):
+    _check(residual.is_contiguous(), "an in-place residual must be contiguous")
+    _gated_residual_impl(mat_a, mat_b, scales_a, scales_b, residual, gate, bias, residual)
 
 
 # --------------------------------------------------------------------------
@@ -532,6 +578,16 @@ def _fake_fp8_scaled_mm_gelu_tanh(mat_a, mat_b, scales_a, scales_b, out_dtype, b
     return mat_a.new_empty((mat_a.shape[0], mat_b.shape[1]), dtype=out_dtype)
 
 
+@torch.library.register_fake("joyomni_ops::fp8_scaled_mm_gated_residual")
+def _fake_fp8_scaled_mm_gated_residual(mat_a, mat_b, scales_a, scales_b, residual, gate, bias=None):
+    return residual.new_empty(residual.shape)
+
+
+@torch.library.register_fake("joyomni_ops::fp8_scaled_mm_gated_residual_")
+def _fake_fp8_scaled_mm_gated_residual_inplace(mat_a, mat_b, scales_a, scales_b, residual, gate, bias=None):
+    return None
+
+
 @torch.library.register_fake("joyomni_ops::fused_qkv_norm_rope_cache")
 def _fake_fused_qkv_norm_rope_cache(qkv, num_heads, eps, q_weight, k_weight, cos, sin, q_out,
                                     k_out, cache_k, cache_v, slot, slot_offset):
@@ -607,6 +663,18 @@ def fp8_scaled_mm_gelu_tanh(mat_a, mat_b, scales_a, scales_b, out_dtype,
                             bias: Optional[torch.Tensor] = None):
     """fp8_scaled_mm followed by GELU-tanh on the rounded output, in one kernel."""
     return _ops.fp8_scaled_mm_gelu_tanh(mat_a, mat_b, scales_a, scales_b, out_dtype, bias)
+
+
+def fp8_scaled_mm_gated_residual(mat_a, mat_b, scales_a, scales_b, residual, gate,
+                                 bias: Optional[torch.Tensor] = None, inplace: bool = False):
+    """residual + fp8_scaled_mm(mat_a, mat_b, ...) * gate in one kernel (the block's out-projection /
+    FFN-down followed by fused_add_gate); output dtype = residual dtype, gate [N]. Bit-identical to
+    ``torch.addcmul(residual, fp8_scaled_mm(...), gate)``. ``inplace=True`` writes into ``residual``
+    (contiguous) and returns it."""
+    if inplace:
+        _ops.fp8_scaled_mm_gated_residual_(mat_a, mat_b, scales_a, scales_b, residual, gate, bias)
+        return residual
+    return _ops.fp8_scaled_mm_gated_residual(mat_a, mat_b, scales_a, scales_b, residual, gate, bias)
 
 
 def fused_qkv_norm_rope_cache(qkv, num_heads, eps, q_weight, k_weight, cos, sin, q_out,

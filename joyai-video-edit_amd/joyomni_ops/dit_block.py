@@ -21,9 +21,11 @@ per stream (video "img", condition "txt"), with ``mod = table + vec`` split into
   (``fused_joint_qkv_pack``, ``dit.py:489-496``);
 * attention: PyTorch SDPA, non-causal, no mask (``dit.py:154-167``), restricted to
   its fused flash / memory-efficient kernels;
-* out-proj FP8 GEMM and gated residual (``fused_add_gate``, ``dit.py:525-528``);
+* out-proj FP8 GEMM with the gated residual (``fused_add_gate``, ``dit.py:525-528``)
+  in its epilogue (``fp8_scaled_mm_gated_residual``);
 * adaLN + FP8 quant -> FFN-up FP8 GEMM with the GELU-tanh epilogue -> quant ->
-  FFN-down FP8 GEMM -> gated residual (``dit.py:508-513,529-538``).
+  FFN-down FP8 GEMM with the gated residual in its epilogue, in place on the
+  stream (``dit.py:508-513,529-538``).
 
 Activation quantiser rounding per K follows the reference's ROCm path
 (``fp8_linear.py:57-74``): reciprocal-multiply below K = 8192, division above.
@@ -141,11 +143,6 @@ class QuantizedDoubleStreamBlock:
         return q, s
 
     @staticmethod
-    def gated_residual(x: torch.Tensor, y: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
-        """fused_add_gate (sgl_fused_ops.py:302-305): x + y * gate."""
-        return torch.addcmul(x, y, gate.unsqueeze(1))
-
-    @staticmethod
     def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
         """SDPA on [B, S, H, D] operands (dit.py:154-167), fused kernels only."""
         from torch.nn.attention import SDPBackend, sdpa_kernel
@@ -220,10 +217,10 @@ class QuantizedDoubleStreamBlock:
 
         outs = []
         for x2d, w, m, a in ((img2, self.img, im, attn[0, :L]), (txt2, self.txt, tm, attn[0, L:])):
-            x = self.gated_residual(x2d[None], w.proj(a)[None], m[2])[0]
+            x = w.proj.gated_residual(a, x2d, m[2])            # new tensor: the caller's input stays
             q8, s8 = self.norm_quant(x, m[3], m[4], E)
             h = w.up.gemm(q8, s8)
-            x = self.gated_residual(x[None], w.down(h)[None], m[5])[0]
+            w.down.gated_residual(h, x, m[5], inplace=True)
             outs.append(x)
         mark("proj_ffn")
         return outs[0].reshape(1, L, E), outs[1].reshape(1, T, E)

@@ -28,7 +28,8 @@ from typing import Optional
 import torch
 import torch.nn as nn
 
-from . import fp8_scaled_mm, fp8_scaled_mm_gelu_tanh, has_fp8, has_quant, per_token_quant_fp8
+from . import (fp8_scaled_mm, fp8_scaled_mm_gated_residual, fp8_scaled_mm_gelu_tanh, has_fp8, has_quant,
+               per_token_quant_fp8)
 
 FP8_DTYPE = torch.float8_e4m3fn
 FP8_MAX = torch.finfo(FP8_DTYPE).max
@@ -106,6 +107,23 @@ class Fp8Linear(nn.Module):
         """The GEMM (+ fused epilogue) on already quantised activations [M, K]."""
         mm = fp8_scaled_mm_gelu_tanh if self.gelu_tanh else fp8_scaled_mm
         return mm(x_q, self.weight_fp8, x_scale, self.weight_scale, self.out_dtype, self.bias)
+
+    def gemm_gated_residual(self, x_q: torch.Tensor, x_scale: torch.Tensor, residual: torch.Tensor,
+                            gate: torch.Tensor, inplace: bool = False) -> torch.Tensor:
+        """residual + gemm(x_q, x_scale) * gate with the gated residual in the GEMM epilogue
+        (the block's fused_add_gate, sgl_fused_ops.py:302-305); residual [M, N]."""
+        assert not self.gelu_tanh, "the gated-residual epilogue has no GELU"
+        assert residual.dtype == self.out_dtype, "residual dtype must be the output dtype"
+        return fp8_scaled_mm_gated_residual(x_q, self.weight_fp8, x_scale, self.weight_scale, residual,
+                                            gate, self.bias, inplace)
+
+    def gated_residual(self, x: torch.Tensor, residual: torch.Tensor, gate: torch.Tensor,
+                       inplace: bool = False) -> torch.Tensor:
+        """residual + self(x) * gate: x [M, K] quantised per token, then one GEMM launch."""
+        x_2d = x.reshape(-1, x.shape[-1]).contiguous()
+        assert x_2d.shape[1] == self.in_features, f"in features mismatch {x_2d.shape[1]} vs {self.in_features}"
+        x_q, x_scale = quantize_per_token(x_2d, self.exact_division)
+        return self.gemm_gated_residual(x_q, x_scale, residual, gate, inplace)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         orig_shape = x.shape

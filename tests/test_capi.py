@@ -70,6 +70,19 @@ def test_gemm_argument_checks(lib):
     assert lib.joy_fp8_scaled_mm(*args(M=0)) == 0
 
 
+def test_gated_residual_argument_checks(lib):
+    p, r, g = ctypes.c_void_p(0x1000), ctypes.c_void_p(0x2000), ctypes.c_void_p(0x3000)
+    args = lambda **kw: [p, p, p, p, None, kw.get("r", r), kw.get("ld", 64), kw.get("g", g),  # noqa: E731
+                         kw.get("out", p), 0, kw.get("M", 64), 64, 64, None]
+    f = lib.joy_fp8_scaled_mm_gated_residual
+    _status(lib, f(*args(r=None)), 1, "residual must be non-null")
+    _status(lib, f(*args(g=None)), 1, "gate must be non-null")
+    _status(lib, f(*args(ld=32)), 1, "row stride must be >= N")
+    _status(lib, f(*args(out=r, ld=72)), 1, "in-place residual must have row stride N")
+    _status(lib, f(*args(r=ctypes.c_void_p(0x2001))), 1, "naturally aligned")
+    assert f(*args(M=0)) == 0
+
+
 def test_norm_rope_argument_checks(lib):
     p = ctypes.c_void_p(0x1000)
     _status(lib, lib.joy_fused_qk_norm_rope_3d_paired(p, p, 1, 4, 2, 96, 1e-6, p, p, p, p, None, None),

@@ -83,6 +83,28 @@ def test_exact_small_integers_bit_exact(M, N, K):
     assert np.array_equal(u16(gemm(qa, qw, sa, sw, None)), exp_nb)
 
 
+@pytest.mark.parametrize("M,N,K", [(300, 264, 256), (64, 520, 384), (33, 40, 48), (520, 4104, 128)])
+def test_fp16_output_with_denormal_bias(M, N, K):
+    """fp16 output, a quarter of the fp16 bias values denormal (k * 2^-24): the zero
+    activation rows output the bias itself, so a flushed denormal shows; exact small
+    integers fix every other output bit too."""
+    announce("gemm fp16 denormal bias", M, N, K)
+    rng = np.random.default_rng(M + 5 * N)
+    qa = f32_to_e4m3fn(rng.integers(-8, 9, (M, K)).astype(np.float32))
+    qa[::5] = 0
+    qw = f32_to_e4m3fn(rng.integers(-8, 9, (N, K)).astype(np.float32))
+    sa = (2.0 ** rng.integers(-8, -2, M)).astype(np.float32)
+    sw = (2.0 ** rng.integers(-8, -2, N)).astype(np.float32)
+    b = (rng.integers(-64, 64, N) / 16).astype(np.float32)
+    den = rng.random(N) < 0.25
+    b[den] = rng.integers(1, 1024, int(den.sum())) * 2.0 ** -24 * rng.choice([-1, 1], int(den.sum()))
+    bias = b.astype(np.float16).view(np.uint16)
+    exp_bits, _ = og.scaled_mm(qa, qw, sa, sw, bias, out_dtype="fp16")
+    y = u16(gemm(qa, qw, sa, sw, bias, out_dtype=torch.float16))
+    assert np.array_equal(y[::5], np.broadcast_to(bias, y[::5].shape))
+    assert np.array_equal(y, exp_bits), f"{np.count_nonzero(y != exp_bits)} outputs differ"
+
+
 @pytest.mark.parametrize("M,N", [(4352, 4096), (5376, 4096)])
 def test_exact_full_rounds_plus_split_tail(M, N):
     """More 256x256 tiles than CUs: full rounds run as 256x256 tiles and the last,

@@ -140,6 +140,28 @@ def test_norm_fp8_matches_separate_quantiser_full_rows(affine):
     assert torch.equal(q.view(torch.uint8), q_ref.view(torch.uint8)) and torch.equal(s, s_ref)
 
 
+@pytest.mark.parametrize("norm_type", ["layer", "rms"])
+@pytest.mark.parametrize("M,N,rows", [(40, 5120, 1), (16, 4096, 16), (8, 2048, 8), (5, 4100, 5)])
+def test_fp16_zero_rows_output_denormal_shift(norm_type, M, N, rows):
+    """A zero input row normalises to 0, so its output is the shift itself: with fp16-denormal
+    shift values a conversion that flushed them would show (every kernel shape)."""
+    import joyomni_ops as jo
+    announce("norm fp16 denormal shift", norm_type, M, N, rows)
+    x, _, _, sc, sh = make(M, N, rows, torch.float16, False, 21 + N)
+    x[::3] = 0
+    sh_bits = u16(sh).copy()
+    sh_bits[:, ::4] = np.random.default_rng(N).integers(1, 1024, sh_bits[:, ::4].shape).astype(np.uint16)
+    sh = torch.from_numpy(sh_bits.view(np.int16)).view(torch.float16)
+    y = jo.fused_norm_scale_shift(dev(x), None, None, dev(sc), dev(sh), norm_type, 1e-6)
+    torch.cuda.synchronize()
+    yb = u16(y)
+    exp_rows = np.broadcast_to(sh_bits, (M, N))[::3]
+    assert np.array_equal(yb[::3], exp_rows)
+    nt = 0 if norm_type == "layer" else 1
+    exp = onm.norm_scale_shift(bits(x), None, None, bits(sc), sh_bits, nt, 1e-6, "fp16")
+    assert_close(yb, exp, (x, None, None, sc, sh), torch.float16, norm_type, "denormal shift")
+
+
 def test_norm_argument_errors():
     import joyomni_ops as jo
     announce("norm argument errors")

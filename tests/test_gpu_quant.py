@@ -66,6 +66,24 @@ def test_fp16_and_ragged_k(variant):
         check(torch.randn(9, K, generator=gen(K)).to(torch.bfloat16), variant)
 
 
+@pytest.mark.parametrize("variant", ["div", "rcp"])
+@pytest.mark.parametrize("K", [2048, 12288, 16384])
+def test_fp16_denormal_inputs(variant, K):
+    """fp16 rows with a small absmax, where fp16 denormal inputs (|x| < 2^-14) quantise to
+    nonzero fp8 bytes: a conversion that flushed them would write 0. K = 16384 is the
+    widest row kept in registers."""
+    announce("quant fp16 denormals", variant, K)
+    g = gen(K + 3)
+    x = torch.randn(16, K, generator=g) * 1e-3
+    x[:, ::7] = (torch.rand(16, x[:, ::7].shape[1], generator=g) - 0.5) * 2.0 ** -13
+    x = x.to(torch.float16)
+    bits = u16(x)
+    den = ((bits & 0x7C00) == 0) & ((bits & 0x3FF) != 0)
+    qr, _ = oq.quant_per_token(bits, "fp16", variant)
+    assert den.mean() > 0.1 and np.count_nonzero(qr[den] & 0x7F) > 0.9 * den.sum()
+    check(x, variant)
+
+
 def test_every_bf16_value_against_many_scales():
     """Every finite bf16 pattern is quantised under scales spanning the whole
     range: rows hold all |x| <= a plus a itself (fixing the row absmax)."""
