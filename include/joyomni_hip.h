@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define JOY_ABI_VERSION 4
+#define JOY_ABI_VERSION 5
 
 #if defined(__GNUC__) || defined(__clang__)
 #define JOY_API __attribute__((visibility("default")))
@@ -133,8 +133,9 @@ JOY_API joy_status joy_fused_qk_norm_rope_3d_paired(void *q, void *k, int64_t ba
  *                                                                 joyomni_ops/csrc/fused_qknorm_rope_3d_kernel.cu:44-106
  *   the cache write of pre-RoPE K and compact V                   deploy/xvideo/models/dit/dit.py:446-451,867-882
  * qkv: bf16 [seq_len, 3*num_heads*head_dim] with row stride qkv_row_stride (elements).
- * q_out, k_out: bf16 [seq_len, num_heads, head_dim] with token strides (elements);
- *   k_out may be NULL.
+ * q_out, k_out, v_out: bf16 [seq_len, num_heads, head_dim] with token strides (elements);
+ *   k_out and v_out may be NULL. v_out receives V itself (e.g. the video rows of the
+ *   joint attention V, dit.py:489-496), so the joint pack need not copy them.
  * cache_k, cache_v: bf16 rings [num_slots, slot_capacity, num_heads, head_dim]
  *   (either both NULL or both set); tokens go to rows slot_offset .. slot_offset+seq_len-1
  *   of slot `slot`: cache_k gets the normalised pre-RoPE K, cache_v a copy of V.
@@ -144,6 +145,7 @@ JOY_API joy_status joy_fused_qkv_norm_rope_cache(const void *qkv, int64_t qkv_ro
                                          const void *q_weight, const void *k_weight,
                                          const void *cos, const void *sin, void *q_out,
                                          int64_t q_out_stride, void *k_out, int64_t k_out_stride,
+                                         void *v_out, int64_t v_out_stride,
                                          void *cache_k, void *cache_v, int64_t num_slots,
                                          int64_t slot_capacity, int64_t slot, int64_t slot_offset,
                                          void *stream);
@@ -186,6 +188,23 @@ JOY_API joy_status joy_fused_joint_qkv_pack(const joy_bf16_view *img_q, const jo
                                     void *out_v, void *stream);
 
 /*
+ * The condition (text) segment of the joint pack, written where the caller says
+ * (new op): with the video rows of the joint Q/K/V written by
+ * joy_fused_qkv_norm_rope_cache and the cached rows by joy_fused_cached_kv_pack,
+ * this completes the joint attention operands of fused_joint_qkv_pack
+ * (joyomni_ops/csrc/fused_joint_qkv_pack.cu:81-164,237-342; dit.py:489-496) without
+ * copying the cached and video rows a second time.
+ *   out_q = rms(txt_q), out_k = rms(txt_k), out_v = txt_v     dense [txt_len, H, D] each
+ *   rms(x) = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w)        (two roundings, :58-79)
+ * Argument rules as joy_fused_joint_qkv_pack (head_dim 128, txt_len, num_heads > 0).
+ */
+JOY_API joy_status joy_fused_text_qkv_pack(const joy_bf16_view *txt_q, const joy_bf16_view *txt_k,
+                                   const joy_bf16_view *txt_v, const void *txt_q_weight,
+                                   const void *txt_k_weight, float eps, int64_t num_heads,
+                                   int64_t head_dim, void *out_q, void *out_k, void *out_v,
+                                   void *stream);
+
+/*
  * Rotate and pack one or two pre-RoPE cached K segments with their V.
  * Replaces: fused_cached_kv_pack(Tensor key0, Tensor value0, Tensor? key1, Tensor? value1,
  *           Tensor cos, Tensor sin) -> (Tensor, Tensor)
@@ -196,8 +215,9 @@ JOY_API joy_status joy_fused_joint_qkv_pack(const joy_bf16_view *img_q, const jo
  *   out_v[t] = value[t]; t runs over key0's tokens, then key1's.
  * cos, sin: fp32 [len0 + len1, head_dim] (full width, repeat_interleave layout).
  * key1/value1: NULL (or ptr NULL) for one segment; both or neither.
- * Outputs: caller-allocated dense [len0 + len1, H, D]. A ring slot (rows of
- * cache_k[slot]) is a valid key view, so this reads the KV ring directly.
+ * Outputs: caller-allocated dense [len0 + len1, H, D], e.g. the cached rows at the
+ * head of the joint attention K / V. A ring slot (rows of cache_k[slot]) is a valid
+ * key view, so this reads the KV ring directly.
  * head_dim must be 128; len0, num_heads > 0; len1 > 0 when present.
  */
 JOY_API joy_status joy_fused_cached_kv_pack(const joy_bf16_view *key0, const joy_bf16_view *value0,

@@ -174,6 +174,7 @@ joy_status joy_fused_qkv_norm_rope_cache(const void* qkv, int64_t qkv_row_stride
                                          const void* q_weight, const void* k_weight,
                                          const void* cos, const void* sin, void* q_out,
                                          int64_t q_out_stride, void* k_out, int64_t k_out_stride,
+                                         void* v_out, int64_t v_out_stride,
                                          void* cache_k, void* cache_v, int64_t num_slots,
                                          int64_t slot_capacity, int64_t slot, int64_t slot_offset,
                                          void* stream) {
@@ -183,8 +184,8 @@ joy_status joy_fused_qkv_norm_rope_cache(const void* qkv, int64_t qkv_row_stride
   if (num_heads > 0x7fffffffLL) return fail(JOY_ERR_UNSUPPORTED, "num_heads too large");
   const int64_t E = num_heads * head_dim;
   if (qkv_row_stride < 3 * E) return fail(JOY_ERR_INVALID_ARGUMENT, "qkv row stride must be >= 3*num_heads*head_dim");
-  if (q_out_stride < E || (k_out && k_out_stride < E))
-    return fail(JOY_ERR_INVALID_ARGUMENT, "q_out/k_out token stride must be >= num_heads*head_dim");
+  if (q_out_stride < E || (k_out && k_out_stride < E) || (v_out && v_out_stride < E))
+    return fail(JOY_ERR_INVALID_ARGUMENT, "q_out/k_out/v_out token stride must be >= num_heads*head_dim");
   if ((cache_k == nullptr) != (cache_v == nullptr))
     return fail(JOY_ERR_INVALID_ARGUMENT, "cache_k and cache_v must be provided together");
   if (cache_k) {
@@ -202,9 +203,11 @@ joy_status joy_fused_qkv_norm_rope_cache(const void* qkv, int64_t qkv_row_stride
     return fail(JOY_ERR_UNSUPPORTED, "seq_len*num_heads above 2^31 - 2^20");
   if (!qkv || !q_out || !q_weight || !k_weight || !cos || !sin)
     return fail(JOY_ERR_INVALID_ARGUMENT, "qkv, q_out, weights and cos/sin must be non-null");
-  if ((qkv_row_stride % 8) || (q_out_stride % 8) || (k_out && (k_out_stride % 8)))
+  if ((qkv_row_stride % 8) || (q_out_stride % 8) || (k_out && (k_out_stride % 8)) ||
+      (v_out && (v_out_stride % 8)))
     return fail(JOY_ERR_UNSUPPORTED, "token strides must be multiples of 8 elements");
   if (!aligned(qkv, 16) || !aligned(q_out, 16) || (k_out && !aligned(k_out, 16)) ||
+      (v_out && !aligned(v_out, 16)) ||
       (cache_k && (!aligned(cache_k, 16) || !aligned(cache_v, 16))) || !aligned(q_weight, 16) ||
       !aligned(k_weight, 16) || !aligned(cos, 8) || !aligned(sin, 8))
     return fail(JOY_ERR_UNSUPPORTED, "tensors must be 16-byte aligned (cos/sin 8-byte)");
@@ -212,7 +215,7 @@ joy_status joy_fused_qkv_norm_rope_cache(const void* qkv, int64_t qkv_row_stride
   joy::NormRopeArgs a;
   a.q_in = base;
   a.k_in = base + E;
-  a.v_in = cache_v ? base + 2 * E : nullptr;
+  a.v_in = (cache_v || v_out) ? base + 2 * E : nullptr;
   a.in_stride = qkv_row_stride;
   a.q_out = (uint16_t*)q_out;
   a.q_out_stride = q_out_stride;
@@ -223,6 +226,8 @@ joy_status joy_fused_qkv_norm_rope_cache(const void* qkv, int64_t qkv_row_stride
   a.kpre_stride = E;
   a.v_out = cache_v ? (uint16_t*)cache_v + slot_base : nullptr;
   a.v_out_stride = E;
+  a.v_out2 = (uint16_t*)v_out;
+  a.v_out2_stride = v_out_stride;
   a.q_weight = (const uint16_t*)q_weight;
   a.k_weight = (const uint16_t*)k_weight;
   a.cos = (const uint16_t*)cos;
@@ -374,6 +379,41 @@ joy_status joy_fused_joint_qkv_pack(const joy_bf16_view* img_q, const joy_bf16_v
   a.heads = (int)num_heads;
   a.eps = eps;
   return hip_status(joy::launch_joint_qkv_pack(a, (hipStream_t)stream), "fused_joint_qkv_pack launch");
+}
+
+joy_status joy_fused_text_qkv_pack(const joy_bf16_view* txt_q, const joy_bf16_view* txt_k,
+                                   const joy_bf16_view* txt_v, const void* txt_q_weight,
+                                   const void* txt_k_weight, float eps, int64_t num_heads,
+                                   int64_t head_dim, void* out_q, void* out_k, void* out_v, void* stream) {
+  // the condition segment of fused_joint_qkv_pack, with its checks (fused_joint_qkv_pack.cu:246-284)
+  if (!present(txt_q) || !present(txt_k) || !present(txt_v))
+    return fail(JOY_ERR_INVALID_ARGUMENT, "txt q, k, v must be non-null");
+  if (head_dim != 128) return fail(JOY_ERR_INVALID_ARGUMENT, "fused_text_qkv_pack requires head_dim=128");
+  const int64_t txt_len = txt_q->len;
+  if (txt_len <= 0 || num_heads <= 0 || txt_k->len != txt_len || txt_v->len != txt_len)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "text Q/K/V lengths must match and be positive");
+  if (!txt_q_weight || !txt_k_weight)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "txt_q_weight and txt_k_weight must be non-null");
+  if (!out_q || !out_k || !out_v) return fail(JOY_ERR_INVALID_ARGUMENT, "out_q, out_k and out_v must be non-null");
+  if (num_heads > 0x7fffffffLL) return fail(JOY_ERR_UNSUPPORTED, "num_heads too large");
+  if (3 * txt_len * num_heads > kMaxPackRows) return fail(JOY_ERR_UNSUPPORTED, "too many rows for one launch");
+  joy::JointPackArgs a;
+  a.img_q = a.img_k = a.img_v = row_view(nullptr);
+  a.cache_k = a.cache_v = row_view(nullptr);
+  a.txt_q = row_view(txt_q);
+  a.txt_k = row_view(txt_k);
+  a.txt_v = row_view(txt_v);
+  a.txt_q_weight = (const uint16_t*)txt_q_weight;
+  a.txt_k_weight = (const uint16_t*)txt_k_weight;
+  a.out_q = (uint16_t*)out_q;
+  a.out_k = (uint16_t*)out_k;
+  a.out_v = (uint16_t*)out_v;
+  a.img_len = 0;
+  a.txt_len = txt_len;
+  a.cache_len = 0;
+  a.heads = (int)num_heads;
+  a.eps = eps;
+  return hip_status(joy::launch_joint_qkv_pack(a, (hipStream_t)stream), "fused_text_qkv_pack launch");
 }
 
 joy_status joy_fused_cached_kv_pack(const joy_bf16_view* key0, const joy_bf16_view* value0,

@@ -20,6 +20,8 @@ struct NormRopeArgs {
   int64_t kpre_stride;
   uint16_t* v_out;  // may be null (requires v_in)
   int64_t v_out_stride;
+  uint16_t* v_out2 = nullptr;  // second V destination (joint attention V rows); may be null
+  int64_t v_out2_stride = 0;
   const uint16_t* q_weight;
   const uint16_t* k_weight;
   const uint16_t* cos;  // [table_len, D/2]

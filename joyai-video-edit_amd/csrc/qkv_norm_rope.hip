@@ -11,8 +11,9 @@
 //  * the reference's in-place op fused_qk_norm_rope_3d_paired (q, k separate
 //    contiguous [B, L*H, D] tensors, outputs over the inputs);
 //  * the fused op: q, k, v read straight from the QKV GEMM output row
-//    [q(H*D) | k(H*D) | v(H*D)], roped q/k written to the attention operands and
-//    the pre-RoPE k and v written into a slot of the KV ring.
+//    [q(H*D) | k(H*D) | v(H*D)], roped q/k written to the attention operands,
+//    the pre-RoPE k and v written into a slot of the KV ring and, optionally, v
+//    also into the attention V operand.
 // Every pointer is a token-strided [tokens, H, D] view, so outputs can land in
 // any caller-owned buffer (ring slot, joint attention buffer) with no copy.
 //
@@ -139,6 +140,7 @@ __global__ __launch_bounds__(512) void qk_norm_rope_kernel(NormRopeArgs a) {
     if (a.k_out) st16<NT>(a.k_out + t * a.k_out_stride + hoff[r], pack_bf16x8(ko));
     if (a.kpre_out) st16<NT>(a.kpre_out + t * a.kpre_stride + hoff[r], pack_bf16x8(k));
     if (a.v_out) st16<NT>(a.v_out + t * a.v_out_stride + hoff[r], vv[r]);
+    if (a.v_out2) st16<NT>(a.v_out2 + t * a.v_out2_stride + hoff[r], vv[r]);
   }
 }
 

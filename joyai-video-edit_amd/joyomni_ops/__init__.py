@@ -44,6 +44,8 @@ __all__ = [
     "fused_qkv_norm_rope_cache",
     "fused_norm_scale_shift_fp8",
     "fp8_scaled_mm_gated_residual",
+    "fused_cached_kv_pack_out",
+    "fused_text_qkv_pack",
 ]
 
 _NS = "joyomni_ops"
@@ -88,7 +90,13 @@ _lib_def.define(
 _lib_def.define(
     "fused_qkv_norm_rope_cache(Tensor qkv, int num_heads, float eps, Tensor q_weight, "
     "Tensor k_weight, Tensor cos, Tensor sin, Tensor(a!) q_out, Tensor(b!)? k_out, "
-    "Tensor(c!)? cache_k, Tensor(d!)? cache_v, int slot, int slot_offset) -> ()")
+    "Tensor(c!)? cache_k, Tensor(d!)? cache_v, int slot, int slot_offset, Tensor(e!)? v_out=None) -> ()")
+_lib_def.define(
+    "fused_cached_kv_pack_out(Tensor key0, Tensor value0, Tensor? key1, Tensor? value1, "
+    "Tensor cos, Tensor sin, Tensor(a!) out_k, Tensor(b!) out_v) -> ()")
+_lib_def.define(
+    "fused_text_qkv_pack(Tensor txt_q, Tensor txt_k, Tensor txt_v, Tensor txt_q_weight, "
+    "Tensor txt_k_weight, float eps, Tensor(a!) out_q, Tensor(b!) out_k, Tensor(c!) out_v) -> ()")
 
 _ops = torch.ops.joyomni_ops
 
@@ -298,7 +306,7 @@ def _token_stride(t: torch.Tensor, H: int, D: int, name: str) -> int:
 
 @torch.library.impl(_lib_def, "fused_qkv_norm_rope_cache", "CUDA")
 def _fused_qkv_norm_rope_cache_cuda(qkv, num_heads, eps, q_weight, k_weight, cos, sin, q_out,
-                                    k_out, cache_k, cache_v, slot, slot_offset):
+                                    k_out, cache_k, cache_v, slot, slot_offset, v_out=None):
     _check(qkv.is_cuda, "qkv must be a CUDA tensor")
     _check(qkv.dtype == torch.bfloat16, f"qkv dtype is {qkv.dtype}, expected torch.bfloat16")
     x = qkv[0] if qkv.dim() == 3 else qkv
@@ -316,7 +324,9 @@ def _fused_qkv_norm_rope_cache_cuda(qkv, num_heads, eps, q_weight, k_weight, cos
            "cos/sin shape must be [seq_len, head_dim/2]")
     q_stride = _token_stride(q_out, H, D, "q_out")
     k_stride = _token_stride(k_out, H, D, "k_out") if k_out is not None else 0
-    for name, t in (("q_out", q_out), ("k_out", k_out), ("cache_k", cache_k), ("cache_v", cache_v)):
+    v_stride = _token_stride(v_out, H, D, "v_out") if v_out is not None else 0
+    for name, t in (("q_out", q_out), ("k_out", k_out), ("v_out", v_out), ("cache_k", cache_k),
+                    ("cache_v", cache_v)):
         if t is not None:
             _check(t.is_cuda and t.dtype == torch.bfloat16, f"{name} must be a bf16 CUDA tensor")
     n_slots = cap = 0
@@ -330,8 +340,8 @@ def _fused_qkv_norm_rope_cache_cuda(qkv, num_heads, eps, q_weight, k_weight, cos
     with torch.cuda.device(qkv.device):
         st = _LIB.joy_fused_qkv_norm_rope_cache(
             _ptr(x), x.stride(0), L, H, D, float(eps), _ptr(q_weight), _ptr(k_weight), _ptr(cos),
-            _ptr(sin), _ptr(q_out), q_stride, _ptr(k_out), k_stride, _ptr(cache_k), _ptr(cache_v),
-            n_slots, cap, int(slot), int(slot_offset), _stream(qkv))
+            _ptr(sin), _ptr(q_out), q_stride, _ptr(k_out), k_stride, _ptr(v_out), v_stride, _ptr(cache_k),
+            _ptr(cache_v), n_slots, cap, int(slot), int(slot_offset), _stream(qkv))
     _lib.check(_LIB, st)
 
 
@@ -400,8 +410,7 @@ def _fused_joint_qkv_pack_cuda(img_q, img_k, img_v, txt_q, txt_k, txt_v, cached_
     return out_q, out_k, out_v
 
 
-@torch.library.impl(_lib_def, "fused_cached_kv_pack", "CUDA")
-def _fused_cached_kv_pack_cuda(key0, value0, key1, value1, cos, sin):
+def _cached_pack_checks(key0, value0, key1, value1, cos, sin):
     # checks of fused_joint_qkv_pack.cu:351-381
     _check(key0.dim() == 4, "key0 must be [B,L,H,D]")
     batch, len0, heads, head_dim = key0.shape
@@ -424,15 +433,65 @@ def _fused_cached_kv_pack_cuda(key0, value0, key1, value1, cos, sin):
     _check(cos.shape == sin.shape, "cos/sin shapes must match")
     _check(cos.numel() == (len0 + len1) * head_dim,
            f"cos/sin must contain [total_cache_len, head_dim], got {list(cos.shape)}")
-    out_k = key0.new_empty((batch, len0 + len1, heads, head_dim))
-    out_v = torch.empty_like(out_k)
+    return len0 + len1, heads, head_dim
+
+
+def _cached_pack_launch(key0, value0, key1, value1, cos, sin, heads, head_dim, out_k, out_v):
     views = [_view(t) for t in (key0, value0, key1, value1)]
     with torch.cuda.device(key0.device):
         st = _LIB.joy_fused_cached_kv_pack(
             *[_vref(v) for v in views], _ptr(cos), _ptr(sin), heads, head_dim, _ptr(out_k), _ptr(out_v),
             _stream(key0))
     _lib.check(_LIB, st)
+
+
+@torch.library.impl(_lib_def, "fused_cached_kv_pack", "CUDA")
+def _fused_cached_kv_pack_cuda(key0, value0, key1, value1, cos, sin):
+    total, heads, head_dim = _cached_pack_checks(key0, value0, key1, value1, cos, sin)
+    out_k = key0.new_empty((1, total, heads, head_dim))
+    out_v = torch.empty_like(out_k)
+    _cached_pack_launch(key0, value0, key1, value1, cos, sin, heads, head_dim, out_k, out_v)
     return out_k, out_v
+
+
+def _check_dense_out(t, name, length, heads, head_dim):
+    """A caller-provided pack output: bf16 CUDA [1, length, H, D] (or [length, H, D]), contiguous."""
+    _check(t.is_cuda and t.dtype == torch.bfloat16, f"{name} must be a bf16 CUDA tensor")
+    _check(t.is_contiguous(), f"{name} must be contiguous")
+    x = t[0] if t.dim() == 4 else t
+    _check((t.dim() == 3 or t.size(0) == 1) and tuple(x.shape) == (length, heads, head_dim),
+           f"{name} must be [1, {length}, {heads}, {head_dim}], got {list(t.shape)}")
+
+
+@torch.library.impl(_lib_def, "fused_cached_kv_pack_out", "CUDA")
+def _fused_cached_kv_pack_out_cuda(key0, value0, key1, value1, cos, sin, out_k, out_v):
+    total, heads, head_dim = _cached_pack_checks(key0, value0, key1, value1, cos, sin)
+    _check_dense_out(out_k, "out_k", total, heads, head_dim)
+    _check_dense_out(out_v, "out_v", total, heads, head_dim)
+    _cached_pack_launch(key0, value0, key1, value1, cos, sin, heads, head_dim, out_k, out_v)
+
+
+@torch.library.impl(_lib_def, "fused_text_qkv_pack", "CUDA")
+def _fused_text_qkv_pack_cuda(txt_q, txt_k, txt_v, txt_q_weight, txt_k_weight, eps, out_q, out_k, out_v):
+    _check(txt_q.dim() == 4, "txt_q must be [B,L,H,D]")
+    batch, txt_len, heads, head_dim = txt_q.shape
+    _check(batch == 1, "fused_text_qkv_pack requires batch=1")
+    _check(head_dim == 128, "fused_text_qkv_pack requires head_dim=128")
+    for name, t in (("txt_q", txt_q), ("txt_k", txt_k), ("txt_v", txt_v)):
+        _check_qkv_tensor(t, name, batch, heads, head_dim)
+    _check(txt_len > 0 and heads > 0 and txt_k.size(1) == txt_len and txt_v.size(1) == txt_len,
+           "text Q/K/V lengths must match and be positive")
+    for name, t in (("txt_q_weight", txt_q_weight), ("txt_k_weight", txt_k_weight)):
+        _check_input(t, name, torch.bfloat16)
+        _check(t.dim() == 1 and t.numel() == head_dim, f"{name} must be [head_dim]")
+    for name, t in (("out_q", out_q), ("out_k", out_k), ("out_v", out_v)):
+        _check_dense_out(t, name, txt_len, heads, head_dim)
+    views = [_view(t) for t in (txt_q, txt_k, txt_v)]
+    with torch.cuda.device(txt_q.device):
+        st = _LIB.joy_fused_text_qkv_pack(
+            *[_vref(v) for v in views], _ptr(txt_q_weight), _ptr(txt_k_weight), float(eps), heads, head_dim,
+            _ptr(out_q), _ptr(out_k), _ptr(out_v), _stream(txt_q))
+    _lib.check(_LIB, st)
 
 
 # --------------------------------------------------------------------------
@@ -590,7 +649,17 @@ def _fake_fp8_scaled_mm_gated_residual_inplace(mat_a, mat_b, scales_a, scales_b,
 
 @torch.library.register_fake("joyomni_ops::fused_qkv_norm_rope_cache")
 def _fake_fused_qkv_norm_rope_cache(qkv, num_heads, eps, q_weight, k_weight, cos, sin, q_out,
-                                    k_out, cache_k, cache_v, slot, slot_offset):
+                                    k_out, cache_k, cache_v, slot, slot_offset, v_out=None):
+    return None
+
+
+@torch.library.register_fake("joyomni_ops::fused_cached_kv_pack_out")
+def _fake_fused_cached_kv_pack_out(key0, value0, key1, value1, cos, sin, out_k, out_v):
+    return None
+
+
+@torch.library.register_fake("joyomni_ops::fused_text_qkv_pack")
+def _fake_fused_text_qkv_pack(txt_q, txt_k, txt_v, txt_q_weight, txt_k_weight, eps, out_q, out_k, out_v):
     return None
 
 
@@ -678,7 +747,20 @@ def fp8_scaled_mm_gated_residual(mat_a, mat_b, scales_a, scales_b, residual, gat
 
 
 def fused_qkv_norm_rope_cache(qkv, num_heads, eps, q_weight, k_weight, cos, sin, q_out,
-                              k_out=None, cache_k=None, cache_v=None, slot=0, slot_offset=0):
-    """QKV split + q/k RMSNorm + RoPE in one pass; pre-RoPE K and V land in ring slot `slot`."""
+                              k_out=None, cache_k=None, cache_v=None, slot=0, slot_offset=0, v_out=None):
+    """QKV split + q/k RMSNorm + RoPE in one pass; pre-RoPE K and V land in ring slot `slot`;
+    ``v_out`` (optional) receives V as well, e.g. the video rows of the joint attention V."""
     _ops.fused_qkv_norm_rope_cache(qkv, num_heads, eps, q_weight, k_weight, cos, sin, q_out, k_out,
-                                   cache_k, cache_v, slot, slot_offset)
+                                   cache_k, cache_v, slot, slot_offset, v_out)
+
+
+def fused_cached_kv_pack_out(key0, value0, key1, value1, cos, sin, out_k, out_v):
+    """fused_cached_kv_pack writing into caller-provided dense [1, len0 + len1, H, D] outputs,
+    e.g. the cached rows at the head of the joint attention K / V."""
+    _ops.fused_cached_kv_pack_out(key0, value0, key1, value1, cos, sin, out_k, out_v)
+
+
+def fused_text_qkv_pack(txt_q, txt_k, txt_v, txt_q_weight, txt_k_weight, eps, out_q, out_k, out_v):
+    """The condition segment of fused_joint_qkv_pack (two-rounding q/k RMSNorm, V copied) written
+    into caller-provided dense [1, T, H, D] outputs (the tails of the joint Q / K / V)."""
+    _ops.fused_text_qkv_pack(txt_q, txt_k, txt_v, txt_q_weight, txt_k_weight, eps, out_q, out_k, out_v)

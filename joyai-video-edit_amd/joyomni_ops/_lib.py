@@ -54,11 +54,13 @@ SIGNATURES = {
     "joy_fused_qk_norm_rope_3d_paired": (
         _int, [_vp, _vp, _i64, _i64, _i64, _i64, _f32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "joy_fused_qkv_norm_rope_cache": (
-        _int, [_vp, _i64, _i64, _i64, _i64, _f32, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64,
+        _int, [_vp, _i64, _i64, _i64, _i64, _f32, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _i64,
                _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
     "joy_fused_joint_qkv_pack": (
         _int, [_view, _view, _view, _view, _view, _view, _view, _view, _vp, _vp, _f32, _i64, _i64,
                _vp, _vp, _vp, _vp]),
+    "joy_fused_text_qkv_pack": (
+        _int, [_view, _view, _view, _vp, _vp, _f32, _i64, _i64, _vp, _vp, _vp, _vp]),
     "joy_fused_cached_kv_pack": (
         _int, [_view, _view, _view, _view, _vp, _vp, _i64, _i64, _vp, _vp, _vp]),
     "joy_fused_norm_scale_shift": (
@@ -68,7 +70,7 @@ SIGNATURES = {
                _vp]),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 
 class JoyError(RuntimeError):

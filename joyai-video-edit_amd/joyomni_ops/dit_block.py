@@ -11,14 +11,18 @@ per stream (video "img", condition "txt"), with ``mod = table + vec`` split into
   (``fused_norm_scale_shift_fp8``: ``fused_layernorm_modulate``
   ``sgl_fused_ops.py:46-91`` fused with the ``Fp8Linear`` quantiser);
 * QKV FP8 GEMM (``fp8_scaled_mm``, ``fp8_linear.py:114-141``);
-* video stream: QKV split + q/k RMSNorm + 3-D RoPE + pre-RoPE K / V into a ring
-  slot in one pass (``fused_qkv_norm_rope_cache``, replacing ``dit.py:409-451`` +
-  ``_write_layer_kv_cache`` ``dit.py:867-882``);
-* cached chunks: pre-RoPE K rotated on read straight out of their ring slots
-  with fp32 full-width tables (``fused_cached_kv_pack``, ``_concat_kv_entries``
-  ``dit.py:216-271``);
-* joint Q/K/V pack with the condition stream's two-rounding q/k RMSNorm
-  (``fused_joint_qkv_pack``, ``dit.py:489-496``);
+* the joint attention operands Q = [video | condition], K, V = [cached | video |
+  condition] (``fused_joint_qkv_pack``, ``dit.py:489-496``) are written in place by
+  their producers, so no row is copied twice:
+  - video stream: QKV split + q/k RMSNorm + 3-D RoPE in one pass, roped q/k and V
+    into the joint buffers, pre-RoPE K and V into a ring slot
+    (``fused_qkv_norm_rope_cache``, replacing ``dit.py:409-451`` +
+    ``_write_layer_kv_cache`` ``dit.py:867-882``);
+  - cached chunks: pre-RoPE K rotated on read straight out of their ring slots
+    with fp32 full-width tables into the head of the joint K / V
+    (``fused_cached_kv_pack_out``, ``_concat_kv_entries`` ``dit.py:216-271``);
+  - condition stream: the two-rounding q/k RMSNorm into the tails
+    (``fused_text_qkv_pack``);
 * attention: PyTorch SDPA, non-causal, no mask (``dit.py:154-167``), restricted to
   its fused flash / memory-efficient kernels;
 * out-proj FP8 GEMM with the gated residual (``fused_add_gate``, ``dit.py:525-528``)
@@ -42,8 +46,8 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from . import (fused_cached_kv_pack, fused_joint_qkv_pack, fused_norm_scale_shift_fp8,
-               fused_qkv_norm_rope_cache)
+from . import (fused_cached_kv_pack_out, fused_norm_scale_shift_fp8, fused_qkv_norm_rope_cache,
+               fused_text_qkv_pack)
 from .fp8_linear import Fp8Linear, exact_division_for
 
 NORM_EPS = 1e-6            # dit.py:35
@@ -176,41 +180,40 @@ class QuantizedDoubleStreamBlock:
         txt_qkv = self.txt.qkv.gemm(q8, s8)
         mark("qkv")
 
-        # video q/k norm + RoPE, pre-RoPE K / V into the ring
-        img_q = torch.empty(L, H, D, dtype=torch.bfloat16, device=img.device)
-        img_k = torch.empty_like(img_q)
+        # joint attention operands: Q = [video | condition], K, V = [cached | video | condition]
+        C = sum(ring.lengths[c.slot] for c in cached) if cached else 0
+        q = torch.empty(1, L + T, H, D, dtype=torch.bfloat16, device=img.device)
+        k = torch.empty(1, C + L + T, H, D, dtype=torch.bfloat16, device=img.device)
+        v = torch.empty_like(k)
+
+        # video q/k norm + RoPE into the joint buffers, pre-RoPE K / V into the ring
         if ring is not None and write_slot is not None:
             fused_qkv_norm_rope_cache(img_qkv, H, NORM_EPS, self.img.q_norm, self.img.k_norm, img_cos, img_sin,
-                                      img_q, img_k, ring.k, ring.v, write_slot, 0)
+                                      q[0, :L], k[0, C:C + L], ring.k, ring.v, write_slot, 0, v_out=v[0, C:C + L])
             ring.lengths[write_slot] = L
         else:
             fused_qkv_norm_rope_cache(img_qkv, H, NORM_EPS, self.img.q_norm, self.img.k_norm, img_cos, img_sin,
-                                      img_q, img_k, None, None, 0, 0)
+                                      q[0, :L], k[0, C:C + L], None, None, 0, 0, v_out=v[0, C:C + L])
         mark("qkv_norm_rope")
 
-        # cached chunks rotated on read (one or two segments per launch, as the reference)
-        cached_k = cached_v = None
-        if cached:
-            parts_k, parts_v = [], []
-            for i in range(0, len(cached), 2):
-                seg = cached[i:i + 2]
-                cos = torch.cat([c.cos for c in seg]) if len(seg) > 1 else seg[0].cos
-                sin = torch.cat([c.sin for c in seg]) if len(seg) > 1 else seg[0].sin
-                k1 = ring.key(seg[1].slot) if len(seg) > 1 else None
-                v1 = ring.value(seg[1].slot) if len(seg) > 1 else None
-                pk, pv = fused_cached_kv_pack(ring.key(seg[0].slot), ring.value(seg[0].slot), k1, v1, cos, sin)
-                parts_k.append(pk)
-                parts_v.append(pv)
-            cached_k = parts_k[0] if len(parts_k) == 1 else torch.cat(parts_k, dim=1)
-            cached_v = parts_v[0] if len(parts_v) == 1 else torch.cat(parts_v, dim=1)
+        # cached chunks rotated on read into the head of K / V (one or two segments per launch)
+        off = 0
+        for i in range(0, len(cached), 2):
+            seg = cached[i:i + 2]
+            n = sum(ring.lengths[c.slot] for c in seg)
+            cos = torch.cat([c.cos for c in seg]) if len(seg) > 1 else seg[0].cos
+            sin = torch.cat([c.sin for c in seg]) if len(seg) > 1 else seg[0].sin
+            k1 = ring.key(seg[1].slot) if len(seg) > 1 else None
+            v1 = ring.value(seg[1].slot) if len(seg) > 1 else None
+            fused_cached_kv_pack_out(ring.key(seg[0].slot), ring.value(seg[0].slot), k1, v1, cos, sin,
+                                     k[:, off:off + n], v[:, off:off + n])
+            off += n
         mark("cached_kv")
 
-        # joint Q / K / V
-        iv = img_qkv.view(1, L, 3, H, D)
+        # condition stream: two-rounding q/k RMSNorm into the tails of Q / K / V
         tv = txt_qkv.view(1, T, 3, H, D)
-        q, k, v = fused_joint_qkv_pack(img_q[None], img_k[None], iv[:, :, 2], tv[:, :, 0], tv[:, :, 1],
-                                       tv[:, :, 2], cached_k, cached_v, self.txt.q_norm, self.txt.k_norm,
-                                       NORM_EPS)
+        fused_text_qkv_pack(tv[:, :, 0], tv[:, :, 1], tv[:, :, 2], self.txt.q_norm, self.txt.k_norm, NORM_EPS,
+                            q[:, L:], k[:, C + L:], v[:, C + L:])
         mark("joint_pack")
         attn = self.attention(q, k, v).flatten(2, 3)
         mark("attention")

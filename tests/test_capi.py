@@ -90,14 +90,18 @@ def test_norm_rope_argument_checks(lib):
     _status(lib, lib.joy_fused_qk_norm_rope_3d_paired(p, p, 1, 4, 2, 128, 1e-6, None, p, p, p, None, None),
             1, "non-null")
     f = lib.joy_fused_qkv_norm_rope_cache
-    _status(lib, f(p, 3 * 256, 4, 2, 128, 1e-6, p, p, p, p, p, 256, None, 0, p, None, 4, 16, 0, 0, None),
-            1, "provided together")
-    _status(lib, f(p, 3 * 256, 4, 2, 128, 1e-6, p, p, p, p, p, 256, None, 0, p, p, 4, 16, 4, 0, None),
+    _status(lib, f(p, 3 * 256, 4, 2, 128, 1e-6, p, p, p, p, p, 256, None, 0, None, 0, p, None, 4, 16, 0, 0,
+                   None), 1, "provided together")
+    _status(lib, f(p, 3 * 256, 4, 2, 128, 1e-6, p, p, p, p, p, 256, None, 0, None, 0, p, p, 4, 16, 4, 0, None),
             1, "slot 4 out of range")
-    _status(lib, f(p, 3 * 256, 4, 2, 128, 1e-6, p, p, p, p, p, 256, None, 0, p, p, 4, 16, 1, 13, None),
+    _status(lib, f(p, 3 * 256, 4, 2, 128, 1e-6, p, p, p, p, p, 256, None, 0, None, 0, p, p, 4, 16, 1, 13, None),
             1, "do not fit")
-    _status(lib, f(p, 100, 4, 2, 128, 1e-6, p, p, p, p, p, 256, None, 0, None, None, 0, 0, 0, 0, None),
+    _status(lib, f(p, 100, 4, 2, 128, 1e-6, p, p, p, p, p, 256, None, 0, None, 0, None, None, 0, 0, 0, 0, None),
             1, "row stride")
+    _status(lib, f(p, 3 * 256, 4, 2, 128, 1e-6, p, p, p, p, p, 256, None, 0, p, 128, None, None, 0, 0, 0, 0,
+                   None), 1, "q_out/k_out/v_out token stride")
+    _status(lib, f(p, 3 * 256, 4, 2, 128, 1e-6, p, p, p, p, p, 256, None, 0, ctypes.c_void_p(0x1008), 256,
+                   None, None, 0, 0, 0, 0, None), 2, "16-byte aligned")
 
 
 def test_single_hip_runtime_in_process():
@@ -132,6 +136,19 @@ def test_joint_pack_argument_checks(lib):
             "text Q/K/V lengths must match and be positive")
     _status(lib, f(*img, *txt, None, None, None, w, 1e-6, 2, 128, *out, None), 1, "weight")
     _status(lib, f(None, *img[1:], *txt, None, None, w, w, 1e-6, 2, 128, *out, None), 1, "non-null")
+
+
+def test_text_pack_argument_checks(lib):
+    p = 0x1000
+    f = lib.joy_fused_text_qkv_pack
+    w = ctypes.c_void_p(p)
+    txt = [_v(lib, p, 2) for _ in range(3)]
+    _status(lib, f(*txt, w, w, 1e-6, 2, 64, w, w, w, None), 1, "requires head_dim=128")
+    _status(lib, f(txt[0], _v(lib, p, 3), txt[2], w, w, 1e-6, 2, 128, w, w, w, None), 1,
+            "text Q/K/V lengths must match and be positive")
+    _status(lib, f(*txt, None, w, 1e-6, 2, 128, w, w, w, None), 1, "weight")
+    _status(lib, f(None, *txt[1:], w, w, 1e-6, 2, 128, w, w, w, None), 1, "non-null")
+    _status(lib, f(*txt, w, w, 1e-6, 2, 128, w, None, w, None), 1, "out_q, out_k and out_v")
 
 
 def test_cached_pack_argument_checks(lib):

@@ -164,6 +164,51 @@ def test_cached_pack_from_ring_slots_baseline_size():
     assert_close(u16(ok[0][torch.from_numpy(toks).to(DEV)]), ek, "rotated K")
 
 
+def test_joint_operands_in_place_equal_reference_sequence():
+    """The block's in-place assembly of the joint attention operands -- the fused QKV op
+    writing the video rows (v_out), fused_cached_kv_pack_out rotating two ring slots into
+    the head of K / V, fused_text_qkv_pack writing the tails -- is byte-identical to the
+    reference sequence (fused QKV op into separate q/k, fused_cached_kv_pack, then
+    fused_joint_qkv_pack), writes every row (NaN-filled buffers) and leaves the same ring."""
+    import joyomni_ops as jo
+    announce("joint operands in place")
+    hh, ww, T, H, D, slots = 30, 40, 64, 40, 128, 3
+    L, E, C = hh * ww, H * D, 2 * hh * ww
+    g = gen(12)
+    img_qkv = bf(torch.randn(L, 3 * E, generator=g)).to(DEV)
+    txt_qkv = bf(torch.randn(T, 3 * E, generator=g)).to(DEV)
+    ring_k = bf(torch.randn(slots, L, H, D, generator=g)).to(DEV)
+    ring_v = bf(torch.randn(slots, L, H, D, generator=g)).to(DEV)
+    qn, kn, tqn, tkn = (bf(1 + 0.1 * torch.randn(D, generator=g)).to(DEV) for _ in range(4))
+    _, _, cb, sb = orope.rope_half_tables([2], hh, ww, (44, 42, 42), 10000.0)
+    cos_h = torch.from_numpy(cb.view(np.int16)).view(torch.bfloat16).to(DEV)
+    sin_h = torch.from_numpy(sb.view(np.int16)).view(torch.bfloat16).to(DEV)
+    c32, s32, _, _ = orope.rope_half_tables([0, 1], hh, ww, (44, 42, 42), 10000.0)
+    cos_f = torch.from_numpy(np.repeat(c32, 2, axis=1)).contiguous().to(DEV)
+    sin_f = torch.from_numpy(np.repeat(s32, 2, axis=1)).contiguous().to(DEV)
+    i4, t4 = img_qkv.view(1, L, 3, H, D), txt_qkv.view(1, T, 3, H, D)
+    # reference sequence
+    rk, rv = ring_k.clone(), ring_v.clone()
+    q_img, k_img = (torch.empty(L, H, D, dtype=torch.bfloat16, device=DEV) for _ in range(2))
+    jo.fused_qkv_norm_rope_cache(img_qkv, H, 1e-6, qn, kn, cos_h, sin_h, q_img, k_img, rk, rv, 2, 0)
+    ck, cv = jo.fused_cached_kv_pack(rk[0][None], rv[0][None], rk[1][None], rv[1][None], cos_f, sin_f)
+    Q, K, V = jo.fused_joint_qkv_pack(q_img[None], k_img[None], i4[:, :, 2], t4[:, :, 0], t4[:, :, 1],
+                                      t4[:, :, 2], ck, cv, tqn, tkn, 1e-6)
+    # in place
+    q = torch.full((1, L + T, H, D), float("nan"), dtype=torch.bfloat16, device=DEV)
+    k = torch.full((1, C + L + T, H, D), float("nan"), dtype=torch.bfloat16, device=DEV)
+    v = torch.full_like(k, float("nan"))
+    jo.fused_qkv_norm_rope_cache(img_qkv, H, 1e-6, qn, kn, cos_h, sin_h, q[0, :L], k[0, C:C + L], ring_k, ring_v,
+                                 2, 0, v_out=v[0, C:C + L])
+    jo.fused_cached_kv_pack_out(ring_k[0][None], ring_v[0][None], ring_k[1][None], ring_v[1][None], cos_f, sin_f,
+                                k[:, :C], v[:, :C])
+    jo.fused_text_qkv_pack(t4[:, :, 0], t4[:, :, 1], t4[:, :, 2], tqn, tkn, 1e-6, q[:, L:], k[:, C + L:],
+                           v[:, C + L:])
+    torch.cuda.synchronize()
+    assert torch.equal(q, Q) and torch.equal(k, K) and torch.equal(v, V)
+    assert torch.equal(ring_k, rk) and torch.equal(ring_v, rv)
+
+
 def test_pack_argument_errors():
     import joyomni_ops as jo
     announce("pack argument errors")
@@ -178,3 +223,8 @@ def test_pack_argument_errors():
         jo.fused_cached_kv_pack(x, x, x, None, c, c)
     with pytest.raises(RuntimeError, match="total_cache_len"):
         jo.fused_cached_kv_pack(x, x, x, x, c, c)
+    with pytest.raises(RuntimeError, match=r"out_k must be \[1, 4, 2, 128\]"):
+        jo.fused_cached_kv_pack_out(x, x, None, None, c, c, x[:, :3], x)
+    with pytest.raises(RuntimeError, match="out_v must be contiguous"):
+        wide = torch.zeros(1, 4, 4, 128, dtype=torch.bfloat16, device=DEV)
+        jo.fused_text_qkv_pack(x, x, x, w, w, 1e-6, x, x, wide[:, :, :2])
