@@ -277,9 +277,14 @@ def bench_small_m(steps, warmup):
             step = Rotation(weights, lambda qw: jo.fp8_scaled_mm(qa, qw.t(), sa, sw.reshape(1, N),
                                                                  torch.bfloat16, bias))
             t = time_launches(step, steps, warmup)
+            # the reference's ROCm GEMM (torch._scaled_mm -> hipBLASLt, fp8_linear.py:124-132), same rotation
+            tr = time_launches(Rotation(weights, lambda qw: torch._scaled_mm(
+                qa, qw.t(), scale_a=sa, scale_b=sw.reshape(1, N), bias=bias, out_dtype=torch.bfloat16,
+                use_fast_accum=True)), steps, warmup)
             b = gemm_bytes(M, N, K)
             out.append({"M": M, "K": K, "N": N, "us": t * 1e6, "gbs": b / t / 1e9,
-                        "frac_hbm_peak": b / t / 1e9 / PEAK_HBM_GBS, "weight_copies": len(weights)})
+                        "frac_hbm_peak": b / t / 1e9 / PEAK_HBM_GBS, "weight_copies": len(weights),
+                        "reference_hipblaslt_us": tr * 1e6, "speedup_vs_reference_gpu": tr / t})
         del weights
     return out
 

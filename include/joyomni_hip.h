@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define JOY_ABI_VERSION 5
+#define JOY_ABI_VERSION 6
 
 #if defined(__GNUC__) || defined(__clang__)
 #define JOY_API __attribute__((visibility("default")))
@@ -85,10 +85,24 @@ JOY_API joy_status joy_per_token_quant_fp8(const void *input, int input_dtype, v
  * Reference rules kept: K % 16 == 0, N % 8 == 0 (16-byte rows), out_dtype bf16/fp16.
  * This build also needs mat_a, mat_b 16-byte aligned and out, scales_b
  * 16-byte aligned (JOY_ERR_UNSUPPORTED otherwise).
+ * workspace: caller-owned device memory for split-K partial sums (16-byte aligned), or
+ *   NULL. With workspace_bytes >= joy_fp8_scaled_mm_workspace_size(M, N, K) the small-M
+ *   plans split K over more blocks (fp32 partials, summed in a fixed order, so results do
+ *   not depend on timing); with less, the same tiles run without the split. Like the
+ *   reference op's output allocation, the torch layer allocates it (fp8_gemm.cu:1486).
  */
 JOY_API joy_status joy_fp8_scaled_mm(const void *mat_a, const void *mat_b, const float *scales_a,
                              const float *scales_b, const void *bias, void *out, int out_dtype,
-                             int64_t M, int64_t N, int64_t K, int epilogue, void *stream);
+                             int64_t M, int64_t N, int64_t K, int epilogue, void *workspace,
+                             int64_t workspace_bytes, void *stream);
+
+/*
+ * Bytes of workspace that joy_fp8_scaled_mm / joy_fp8_scaled_mm_gated_residual can use
+ * for an (M, N, K) problem on the current device; 0 when no plan splits K (then the
+ * workspace argument may be NULL). Negative sizes return 0. No reference counterpart:
+ * the reference's CUTLASS/hipBLASLt GEMMs allocate their own workspaces internally.
+ */
+JOY_API int64_t joy_fp8_scaled_mm_workspace_size(int64_t M, int64_t N, int64_t K);
 
 /*
  * FP8 GEMM with the gated residual of the DiT block fused into its epilogue (new
@@ -99,14 +113,14 @@ JOY_API joy_status joy_fp8_scaled_mm(const void *mat_a, const void *mat_b, const
  *   out[m,n] = round(residual[m,n] + y * gate[n])                        (fp32, one rounding)
  * residual: [M, N] of out_dtype with row stride residual_stride (elements); gate: [N]
  * of out_dtype. out may be residual itself (in place; then residual_stride == N).
- * Argument rules otherwise as joy_fp8_scaled_mm.
+ * Argument rules and workspace otherwise as joy_fp8_scaled_mm.
  */
 JOY_API joy_status joy_fp8_scaled_mm_gated_residual(const void *mat_a, const void *mat_b,
                                             const float *scales_a, const float *scales_b,
                                             const void *bias, const void *residual,
                                             int64_t residual_stride, const void *gate, void *out,
                                             int out_dtype, int64_t M, int64_t N, int64_t K,
-                                            void *stream);
+                                            void *workspace, int64_t workspace_bytes, void *stream);
 
 /*
  * In-place per-head q/k RMSNorm + interleaved RoPE.

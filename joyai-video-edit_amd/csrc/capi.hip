@@ -36,7 +36,7 @@ constexpr int64_t kMaxUnits = 0x7ff00000LL;
 joy_status scaled_mm_common(const void* mat_a, const void* mat_b, const float* scales_a, const float* scales_b,
                             const void* bias, void* out, int out_dtype, int64_t M, int64_t N, int64_t K,
                             int epilogue, const void* residual, int64_t residual_stride, const void* gate,
-                            void* stream) {
+                            void* workspace, int64_t workspace_bytes, void* stream) {
   if (M < 0 || N < 0 || K < 0) return fail(JOY_ERR_INVALID_ARGUMENT, "mat_a and mat_b shapes cannot be multiplied");
   if (K % 16 != 0)
     return fail(JOY_ERR_INVALID_ARGUMENT, "mat_a must be multiple of 16 bytes for memory alignment");
@@ -52,6 +52,10 @@ joy_status scaled_mm_common(const void* mat_a, const void* mat_b, const float* s
   if (residual && !gate) return fail(JOY_ERR_INVALID_ARGUMENT, "gate must be non-null");
   if (residual && residual == out && residual_stride != N)
     return fail(JOY_ERR_INVALID_ARGUMENT, "an in-place residual must have row stride N");
+  if (workspace_bytes < 0 || (workspace_bytes > 0 && !workspace))
+    return fail(JOY_ERR_INVALID_ARGUMENT, "workspace_bytes must be >= 0, with a workspace when > 0");
+  if (workspace && !aligned(workspace, 16))
+    return fail(JOY_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
   if (M == 0 || N == 0) return ok();
   if (!out || !scales_a || !scales_b || (K > 0 && (!mat_a || !mat_b)))
     return fail(JOY_ERR_INVALID_ARGUMENT, "mat_a, mat_b, scales and out must be non-null");
@@ -76,6 +80,8 @@ joy_status scaled_mm_common(const void* mat_a, const void* mat_b, const float* s
   g.residual = residual;
   g.ldr = residual_stride;
   g.gate = gate;
+  g.workspace = workspace;
+  g.workspace_bytes = workspace ? workspace_bytes : 0;
   return hip_status(joy::launch_fp8_gemm(g, (hipStream_t)stream),
                     residual ? "fp8_scaled_mm_gated_residual launch" : "fp8_scaled_mm launch");
 }
@@ -111,18 +117,25 @@ joy_status joy_per_token_quant_fp8(const void* input, int input_dtype, void* out
 
 joy_status joy_fp8_scaled_mm(const void* mat_a, const void* mat_b, const float* scales_a,
                              const float* scales_b, const void* bias, void* out, int out_dtype,
-                             int64_t M, int64_t N, int64_t K, int epilogue, void* stream) {
+                             int64_t M, int64_t N, int64_t K, int epilogue, void* workspace,
+                             int64_t workspace_bytes, void* stream) {
   return scaled_mm_common(mat_a, mat_b, scales_a, scales_b, bias, out, out_dtype, M, N, K, epilogue, nullptr, 0,
-                          nullptr, stream);
+                          nullptr, workspace, workspace_bytes, stream);
+}
+
+int64_t joy_fp8_scaled_mm_workspace_size(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0 || M > 0x7fffffffLL || N > 0x7fffffffLL || K > 0x7fffffffLL) return 0;
+  return joy::fp8_gemm_workspace_bytes((int)M, (int)N, (int)K);
 }
 
 joy_status joy_fp8_scaled_mm_gated_residual(const void* mat_a, const void* mat_b, const float* scales_a,
                                             const float* scales_b, const void* bias, const void* residual,
                                             int64_t residual_stride, const void* gate, void* out, int out_dtype,
-                                            int64_t M, int64_t N, int64_t K, void* stream) {
+                                            int64_t M, int64_t N, int64_t K, void* workspace,
+                                            int64_t workspace_bytes, void* stream) {
   if (!residual) return fail(JOY_ERR_INVALID_ARGUMENT, "residual must be non-null");
   return scaled_mm_common(mat_a, mat_b, scales_a, scales_b, bias, out, out_dtype, M, N, K, JOY_EPILOGUE_NONE,
-                          residual, residual_stride, gate, stream);
+                          residual, residual_stride, gate, workspace, workspace_bytes, stream);
 }
 
 joy_status joy_fused_qk_norm_rope_3d_paired(void* q, void* k, int64_t batch, int64_t seq_len,

@@ -32,6 +32,8 @@
 // other shape with K % 16 == 0.
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "joy_common.hpp"
 #include "joy_kernels.hpp"
 
@@ -111,8 +113,9 @@ struct ResidualArgs {
 };
 
 // Epilogue kinds, a template parameter so that the plain and GELU kernels carry no
-// residual registers.
-enum Epi : int { kEpiPlain = 0, kEpiGelu = 1, kEpiResidual = 2 };
+// residual registers. kEpiPartial writes the raw fp32 accumulators of a K range
+// (split-K) to a workspace; the reduce kernel applies one of the other kinds.
+enum Epi : int { kEpiPlain = 0, kEpiGelu = 1, kEpiResidual = 2, kEpiPartial = 3 };
 
 template <bool kBf16>
 __device__ __forceinline__ uint32_t gated_pair(uint32_t y, uint32_t x, uint32_t g) {
@@ -198,15 +201,18 @@ struct TileCoord {
   int tm, tn;
 };
 
+// XCD-aware position of block b of nblocks: hardware deals workgroups round-robin
+// to the 8 XCDs; give each XCD a contiguous range of positions so its L2 sees
+// neighbouring tiles.
+__device__ __forceinline__ int xcd_position(int b, int nblocks) {
+  const int xcd = b & 7, local = b >> 3, q = nblocks >> 3, rem = nblocks & 7;
+  return xcd < rem ? xcd * (q + 1) + local : rem * (q + 1) + (xcd - rem) * q + local;
+}
+
 __device__ __forceinline__ TileCoord map_tile(int b, int nblocks, int tiles_m, int tiles_n,
                                               int group_m, int base) {
   int t = b;
-  if (nblocks > 0) {
-    // XCD-aware: hardware deals workgroups round-robin to the 8 XCDs; give each XCD
-    // a contiguous range of positions so its L2 sees neighbouring tiles.
-    const int xcd = b & 7, local = b >> 3, q = nblocks >> 3, rem = nblocks & 7;
-    t = xcd < rem ? xcd * (q + 1) + local : rem * (q + 1) + (xcd - rem) * q + local;
-  }
+  if (nblocks > 0) t = xcd_position(b, nblocks);
   t += base;
   // grouped order: group_m tile rows walk the tile columns together
   const int per_group = group_m * tiles_n;
@@ -218,15 +224,22 @@ __device__ __forceinline__ TileCoord map_tile(int b, int nblocks, int tiles_m, i
 }
 
 // LDS rows of the operand ring are KS bytes = KS/16 chunks of 16 bytes; logical
-// chunk c of row r is stored at c ^ swz(r). Both swizzles were chosen by measuring
-// SQ_LDS_BANK_CONFLICT on gfx950 (zero for the fragment reads):
+// chunk c of row r is stored at c ^ swz(r). The KS = 64 and 128 swizzles were chosen
+// by measuring SQ_LDS_BANK_CONFLICT on gfx950 (zero for the fragment reads):
 //   KS = 64:  swz(r) = (r >> 2) & 3
 //   KS = 128: swz(r) = (r & 7) ^ ((r >> 3) & 1)
-// Both are invariant under r -> r + 32, so a lane's fragment rows share its swizzle.
+//   KS >= 256: swz(r) = r & 15 (16 consecutive rows reading one logical chunk hit 16
+//              distinct 16-byte bank groups of a row pitch that is a multiple of 256 B)
+// All are invariant under r -> r + 32, so a lane's fragment rows share its swizzle.
 template <int KS>
 __device__ __forceinline__ int swz_rows(int r) {
-  if constexpr (KS == 64) return (r >> 2) & 3;
-  return (r & 7) ^ ((r >> 3) & 1);
+  if constexpr (KS == 64) {
+    return (r >> 2) & 3;
+  } else if constexpr (KS == 128) {
+    return (r & 7) ^ ((r >> 3) & 1);
+  } else {
+    return r & 15;
+  }
 }
 
 // s_waitcnt with vmcnt(n), expcnt/lgkmcnt at their maxima (gfx9 encoding).
@@ -342,13 +355,133 @@ __device__ __forceinline__ void sched_pattern() {
 // Small-M launch (sub_log2 == -2): BM x BN tiles of a tiles_m x tiles_n grid,
 // M fastest within each XCD's contiguous range (the M tiles of one weight tile
 // run together, so W is fetched once per XCD).
+// Split-K launch (sub_log2 == -3, kEpi == kEpiPartial): BM x BN tiles times
+// `splits` K ranges; position -> (M tile fastest, N tile, split), and split s
+// covers K steps [s*nk/splits, (s+1)*nk/splits). The tile's fp32 sums go to
+// ws[s][m][n] (row-major [M, N] per split) for the reduce kernel.
 // ---------------------------------------------------------------------------
+// Origin and K range of one block's tile.
+struct TileJob {
+  int m0, n0;
+  int k_step0, nk;  // K steps [k_step0, k_step0 + nk) of the kernel's step size
+  int split;
+};
+
+template <int BM, int BN, int KS = 64>
+__device__ __forceinline__ TileJob decode_job(int K, int tiles_m, int tiles_n, int group_m, int tile_base,
+                                              int sub_log2, int splits) {
+  TileJob j;
+  j.k_step0 = 0;
+  j.nk = K / KS;
+  j.split = 0;
+  if (sub_log2 == -3) {
+    int p = xcd_position(blockIdx.x, gridDim.x);
+    const int tm = p % tiles_m;
+    p /= tiles_m;
+    const int tn = p % tiles_n;
+    j.split = p / tiles_n;
+    j.m0 = tm * BM;
+    j.n0 = tn * BN;
+    const int nk_all = j.nk;
+    j.k_step0 = (int)((int64_t)j.split * nk_all / splits);
+    j.nk = (int)((int64_t)(j.split + 1) * nk_all / splits) - j.k_step0;
+  } else if (sub_log2 == -2) {
+    const TileCoord tc = map_tile(blockIdx.x, gridDim.x, tiles_n, tiles_m, 1, 0);
+    j.m0 = tc.tn * BM;
+    j.n0 = tc.tm * BN;
+  } else if (sub_log2 < 0) {
+    const TileCoord tc = map_tile(blockIdx.x, gridDim.x, tiles_m, tiles_n, group_m, 0);
+    j.m0 = tc.tm * 256;
+    j.n0 = tc.tn * 256;
+  } else {
+    const TileCoord tc = map_tile(blockIdx.x >> sub_log2, -1, tiles_m, tiles_n, group_m, tile_base);
+    const int sub = blockIdx.x & ((1 << sub_log2) - 1);
+    constexpr int SUB_M = 256 / BM;
+    j.m0 = tc.tm * 256 + (sub % SUB_M) * BM;
+    j.n0 = tc.tn * 256 + (sub / SUB_M) * BN;
+  }
+  return j;
+}
+
+// Per-wave global addresses of the operand rows for K steps of KS bytes: one load
+// instruction covers RPI = 1024 / KS rows; lane l covers row l / (KS/16) and fetches
+// logical 16-byte chunk (l % (KS/16)) ^ swz(row), which lands in physical chunk
+// l % (KS/16) of that LDS row (so the LDS write is 1 KB contiguous).
+template <int IA, int IW, int KS = 64>
+__device__ __forceinline__ void operand_rows(const uint8_t* A, const uint8_t* W, int M, int N, int K,
+                                             const TileJob& job, int wave, int lane, const uint8_t* (&pa)[IA],
+                                             const uint8_t* (&pw)[IW]) {
+  constexpr int CPR = KS / 16, RPI = 64 / CPR;
+  const int lrow = lane / CPR, lchunk = lane % CPR;
+  const int64_t k0 = (int64_t)job.k_step0 * KS;
+#pragma unroll
+  for (int i = 0; i < IA; ++i) {
+    const int row = (wave * IA + i) * RPI + lrow;
+    pa[i] = A + (int64_t)min(job.m0 + row, M - 1) * K + k0 + (lchunk ^ swz_rows<KS>(row)) * 16;
+  }
+#pragma unroll
+  for (int i = 0; i < IW; ++i) {
+    const int row = (wave * IW + i) * RPI + lrow;
+    pw[i] = W + (int64_t)min(job.n0 + row, N - 1) * K + k0 + (lchunk ^ swz_rows<KS>(row)) * 16;
+  }
+}
+
+// End of a tile: raw fp32 sums to the split-K workspace (kEpiPartial), or the
+// scaled, rounded tile staged through LDS and stored as whole row segments.
+template <bool kBf16, int kEpi, int BM, int BN>
+__device__ __forceinline__ void finish_tile(const v16f (&acc)[BN / 64][BM / 64], const TileJob& job, uint8_t* lds,
+                                            int wave, int lane, int M, int N, const float* __restrict__ sa,
+                                            const float* __restrict__ sb, const uint16_t* __restrict__ bias,
+                                            uint16_t* __restrict__ C, int64_t ldc, const ResidualArgs& res,
+                                            float* __restrict__ ws) {
+  constexpr int WTM = BM / 2, WTN = BN / 2, FM = WTM / 32, FN = WTN / 32;
+  constexpr int STAGE_BYTES = WTM * (WTN * 2 + 16);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int frow = lane & 31, g = lane >> 5;
+  if constexpr (kEpi == kEpiPartial) {
+    // lane (frow, g) holds rows m, columns n..n+3 of each 32x32 tile; 16-byte
+    // stores, 32 contiguous bytes per row and (i, q)
+    wait_vmcnt<0>();  // no load into LDS or registers outlives the block
+    float* wsp = ws + (int64_t)job.split * M * N;
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+      const int m = job.m0 + wm * WTM + j * 32 + frow;
+      if (m >= M) continue;
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int n = job.n0 + wn * WTN + i * 32 + q * 8 + g * 4;
+          if (n < N)
+            *(float4*)(wsp + (int64_t)m * N + n) =
+                make_float4(acc[i][j][q * 4], acc[i][j][q * 4 + 1], acc[i][j][q * 4 + 2], acc[i][j][q * 4 + 3]);
+        }
+    }
+  } else {
+    // epilogue operands; their latency overlaps the drain of the last loads and the barrier
+    ColOperands<FN> col;
+    load_col_operands<FN>(col, job.n0 + wn * WTN, g, N, sb, bias);
+    float sav[FM];
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+      const int m = job.m0 + wm * WTM + j * 32 + frow;
+      sav[j] = m < M ? sa[m] : 0.0f;
+    }
+    // every wave's loads and fragment reads are done before LDS is reused for staging
+    wait_vmcnt<0>();
+    __builtin_amdgcn_s_waitcnt(0x0070);
+    block_barrier();
+    store_tile_lds<kBf16, kEpi, FN, FM>(acc, col, sav, lds + wave * STAGE_BYTES, job.m0 + wm * WTM,
+                                         job.n0 + wn * WTN, lane, C, M, N, ldc, res);
+  }
+}
+
 template <bool kBf16, int kEpi, int BM, int BN, int S>
 __global__ __launch_bounds__(256, 1) void fp8_gemm_4w(
     const uint8_t* __restrict__ A, const uint8_t* __restrict__ W, const float* __restrict__ sa,
     const float* __restrict__ sb, const uint16_t* __restrict__ bias, uint16_t* __restrict__ C,
     int M, int N, int K, int64_t ldc, int tiles_m, int tiles_n, int group_m, int tile_base,
-    int sub_log2, ResidualArgs res) {
+    int sub_log2, ResidualArgs res, float* __restrict__ ws, int splits) {
   constexpr int KS = 64, NW = 4;
   constexpr int WTM = BM / 2, WTN = BN / 2;  // wave sub-tile
   constexpr int FM = WTM / 32, FN = WTN / 32;
@@ -365,39 +498,11 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4w(
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  int m0, n0;
-  if (sub_log2 == -2) {
-    const TileCoord tc = map_tile(blockIdx.x, gridDim.x, tiles_n, tiles_m, 1, 0);
-    m0 = tc.tn * BM;
-    n0 = tc.tm * BN;
-  } else if (sub_log2 < 0) {
-    const TileCoord tc = map_tile(blockIdx.x, gridDim.x, tiles_m, tiles_n, group_m, 0);
-    m0 = tc.tm * 256;
-    n0 = tc.tn * 256;
-  } else {
-    const TileCoord tc = map_tile(blockIdx.x >> sub_log2, -1, tiles_m, tiles_n, group_m, tile_base);
-    const int sub = blockIdx.x & ((1 << sub_log2) - 1);
-    constexpr int SUB_M = 256 / BM;
-    m0 = tc.tm * 256 + (sub % SUB_M) * BM;
-    n0 = tc.tn * 256 + (sub / SUB_M) * BN;
-  }
-
-  // DMA: lane l of an instruction writes LDS row l/4, physical 16-byte chunk l%4,
-  // fetching logical chunk (l%4) ^ swz(row) of that row.
-  const int lrow = lane >> 2, lchunk = lane & 3;
+  const TileJob job = decode_job<BM, BN>(K, tiles_m, tiles_n, group_m, tile_base, sub_log2, splits);
+  const int nk = job.nk;
   const uint8_t* pa[IA];
   const uint8_t* pw[IW];
-#pragma unroll
-  for (int i = 0; i < IA; ++i) {
-    const int row = (wave * IA + i) * RPI + lrow;
-    pa[i] = A + (int64_t)min(m0 + row, M - 1) * K + (lchunk ^ swz_rows<KS>(row)) * 16;
-  }
-#pragma unroll
-  for (int i = 0; i < IW; ++i) {
-    const int row = (wave * IW + i) * RPI + lrow;
-    pw[i] = W + (int64_t)min(n0 + row, N - 1) * K + (lchunk ^ swz_rows<KS>(row)) * 16;
-  }
-  const int nk = K / KS;
+  operand_rows<IA, IW>(A, W, M, N, K, job, wave, lane, pa, pw);
   auto issue = [&](int slot, int kt) {
     const int64_t koff = (int64_t)min(kt, nk - 1) * KS;
     uint8_t* base = lds + slot * SLOT;
@@ -481,21 +586,151 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4w(
   if (kt < nk) {  // odd step count: last step's fragments are in set 0
     mfmas(fw0, fa0);
   }
-  // epilogue operands; their latency overlaps the drain of the last DMAs and the barrier
-  ColOperands<FN> col;
-  load_col_operands<FN>(col, n0 + wn * WTN, g, N, sb, bias);
-  float sav[FM];
-#pragma unroll
-  for (int j = 0; j < FM; ++j) {
-    const int m = m0 + wm * WTM + j * 32 + frow;
-    sav[j] = m < M ? sa[m] : 0.0f;
+  finish_tile<kBf16, kEpi, BM, BN>(acc, job, lds, wave, lane, M, N, sa, sb, bias, C, ldc, res, ws);
+}
+
+template <int J>
+using IC = std::integral_constant<int, J>;
+
+// Calls f(IC<I>{}), ..., f(IC<N-1>{}) (compile-time indices for register arrays).
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(IC<I>{});
+    static_for<I + 1, N>(f);
   }
-  // every wave's DMAs and fragment reads are done before LDS is reused for staging
-  wait_vmcnt<0>();
-  __builtin_amdgcn_s_waitcnt(0x0070);
-  block_barrier();
-  store_tile_lds<kBf16, kEpi, FN, FM>(acc, col, sav, lds + wave * STAGE_BYTES, m0 + wm * WTM,
-                                       n0 + wn * WTN, lane, C, M, N, ldc, res);
+}
+
+// ---------------------------------------------------------------------------
+// Deep-K register-staged kernel for grids of at most a few rounds (small M): the
+// tiles, waves, MFMA fragments, launch modes and epilogue of fp8_gemm_4w, with K
+// steps of KS = 128..512 bytes so that each barrier covers KS/64 MFMA k-steps and
+// each load instruction reads whole 256..512-byte row runs. Small-M GEMMs are
+// bound by the bytes each CU keeps in flight against ~2 us of loaded memory
+// latency; a 64x64 tile with KS = 512 keeps 64 KB per step and block in flight.
+//
+// LDS holds two slots of one K step; U staging buffers of one step live in VGPRs.
+// Iteration t (after one barrier):
+//   * loads step t+U into staging buffer t % U (its previous step t was written
+//     to LDS in iteration t-1),
+//   * runs the MFMAs of step t from slot t % 2, reading the fragments of k-step
+//     s+1 while the MFMAs of k-step s run,
+//   * writes step t+1 (loaded U-1 iterations earlier) into slot (t+1) % 2, which
+//     every wave finished reading in iteration t-1, before this iteration's barrier.
+// ---------------------------------------------------------------------------
+template <bool kBf16, int kEpi, int BM, int BN, int KS, int U>
+__global__ __launch_bounds__(256, 1) void fp8_gemm_4k(
+    const uint8_t* __restrict__ A, const uint8_t* __restrict__ W, const float* __restrict__ sa,
+    const float* __restrict__ sb, const uint16_t* __restrict__ bias, uint16_t* __restrict__ C,
+    int M, int N, int K, int64_t ldc, int tiles_m, int tiles_n, int group_m, int tile_base,
+    int sub_log2, ResidualArgs res, float* __restrict__ ws, int splits) {
+  constexpr int NW = 4;
+  constexpr int WTM = BM / 2, WTN = BN / 2;
+  constexpr int FM = WTM / 32, FN = WTN / 32;
+  constexpr int CPR = KS / 16, RPI = 64 / CPR;
+  constexpr int IA = BM / RPI / NW, IW = BN / RPI / NW;
+  constexpr int A_BYTES = BM * KS, SLOT = (BM + BN) * KS;
+  constexpr int LOADS = IA + IW;
+  constexpr int SUBS = KS / 64;
+  constexpr int UNR = U % 2 == 0 ? U : 2 * U;
+  static_assert(KS >= 128 && KS <= 512, "deep K steps only");
+  static_assert(U >= 2, "at least two staging buffers");
+  static_assert(IA * RPI * NW == BM && IW * RPI * NW == BN, "tile rows must split over waves");
+  constexpr int STAGE_BYTES = WTM * (WTN * 2 + 16);
+  constexpr int LDS_BYTES = 2 * SLOT > NW * STAGE_BYTES ? 2 * SLOT : NW * STAGE_BYTES;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const TileJob job = decode_job<BM, BN, KS>(K, tiles_m, tiles_n, group_m, tile_base, sub_log2, splits);
+  const int nk = job.nk;
+  const uint8_t* pa[IA];
+  const uint8_t* pw[IW];
+  operand_rows<IA, IW, KS>(A, W, M, N, K, job, wave, lane, pa, pw);
+
+  v4i stg[U][LOADS];
+  auto gload = [&](auto bc, int kt) {
+    constexpr int B = decltype(bc)::value;
+    const int64_t koff = (int64_t)min(kt, nk - 1) * KS;
+#pragma unroll
+    for (int i = 0; i < IA; ++i) stg[B][i] = *(const v4i*)(pa[i] + koff);
+#pragma unroll
+    for (int i = 0; i < IW; ++i) stg[B][IA + i] = *(const v4i*)(pw[i] + koff);
+  };
+  auto lwrite = [&](auto bc, int slot) {
+    constexpr int B = decltype(bc)::value;
+    uint8_t* base = lds + slot * SLOT + lane * 16;
+#pragma unroll
+    for (int i = 0; i < IA; ++i) *(v4i*)(base + (wave * IA + i) * 1024) = stg[B][i];
+#pragma unroll
+    for (int i = 0; i < IW; ++i) *(v4i*)(base + A_BYTES + (wave * IW + i) * 1024) = stg[B][IA + i];
+  };
+
+  const int wm = wave >> 1, wn = wave & 1;
+  const int frow = lane & 31, g = lane >> 5;
+  const int fsw = swz_rows<KS>(frow);
+  const int a_row0 = (wm * WTM + frow) * KS, w_row0 = A_BYTES + (wn * WTN + frow) * KS;
+
+  v16f acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j) acc[i][j] = (v16f){};
+
+  v8i fw[2][FN], fa[2][FM];
+  // fragments of k-step ks (64 bytes: logical chunks 4 ks + 2 g and + 1) of the step in `slot`
+  auto read_frags = [&](auto sc, auto kc, int slot) {
+    constexpr int SL = decltype(sc)::value, KK = decltype(kc)::value;
+    const uint8_t* base = lds + slot * SLOT;
+    const int o0 = ((4 * KK + 2 * g) ^ fsw) * 16, o1 = ((4 * KK + 2 * g + 1) ^ fsw) * 16;
+#pragma unroll
+    for (int f = 0; f < FN; ++f) {
+      const uint8_t* r = base + w_row0 + f * 32 * KS;
+      const v4i lo = *(const v4i*)(r + o0);
+      const v4i hi = *(const v4i*)(r + o1);
+      fw[SL][f] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+#pragma unroll
+    for (int f = 0; f < FM; ++f) {
+      const uint8_t* r = base + a_row0 + f * 32 * KS;
+      const v4i lo = *(const v4i*)(r + o0);
+      const v4i hi = *(const v4i*)(r + o1);
+      fa[SL][f] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+  };
+  auto mfmas = [&](auto sc) {
+    constexpr int SL = decltype(sc)::value;
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j) acc[i][j] = mfma_32x32x64_fp8(fw[SL][i], fa[SL][j], acc[i][j]);
+  };
+  auto iteration = [&](auto jc, int t) {
+    constexpr int J = decltype(jc)::value;
+    constexpr int CUR = J & 1;
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): own LDS writes and fragment reads done
+    block_barrier();
+    gload(IC<J % U>{}, t + U);
+    read_frags(IC<0>{}, IC<0>{}, CUR);
+    static_for<1, SUBS>([&](auto kc) {
+      constexpr int KK = decltype(kc)::value;
+      read_frags(IC<KK & 1>{}, kc, CUR);
+      mfmas(IC<(KK - 1) & 1>{});
+    });
+    mfmas(IC<(SUBS - 1) & 1>{});
+    lwrite(IC<(J + 1) % U>{}, CUR ^ 1);
+  };
+
+  // prologue: steps 0..U-1 into the staging buffers, step 0 into slot 0
+  static_for<0, U>([&](auto bc) { gload(bc, decltype(bc)::value); });
+  lwrite(IC<0>{}, 0);
+
+  int kt = 0;
+  for (; kt + UNR <= nk; kt += UNR) static_for<0, UNR>([&](auto jc) { iteration(jc, kt + decltype(jc)::value); });
+  static_for<0, UNR - 1>([&](auto jc) {
+    if (kt + decltype(jc)::value < nk) iteration(jc, kt + decltype(jc)::value);
+  });
+  finish_tile<kBf16, kEpi, BM, BN>(acc, job, lds, wave, lane, M, N, sa, sb, bias, C, ldc, res, ws);
 }
 
 ResidualArgs residual_args(const GemmArgs& g) {
@@ -522,7 +757,6 @@ int device_cus() {
 // not depend on the split (every output element sums its K products in the same order).
 template <bool kBf16, int kEpi>
 hipError_t launch_4w(const GemmArgs& g, hipStream_t st) {
-  constexpr int S = 5;
   const int tiles_m = (g.M + 255) / 256, tiles_n = (g.N + 255) / 256;
   const int T = tiles_m * tiles_n, P = device_cus();
   int rem = T % P;
@@ -534,49 +768,179 @@ hipError_t launch_4w(const GemmArgs& g, hipStream_t st) {
   } else {
     rem = 0;  // the last round is nearly full: no split
   }
+  constexpr int D = 5;  // DMA ring depth
   const int bulk = T - rem;
   if (bulk > 0) {
-    hipLaunchKernelGGL((fp8_gemm_4w<kBf16, kEpi, 256, 256, S>), dim3(bulk), dim3(256), 0, st,
-                       (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a, g.scales_b,
-                       (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tiles_m, tiles_n,
-                       kGroupM, 0, -1, residual_args(g));
+    auto kern = fp8_gemm_4w<kBf16, kEpi, 256, 256, D>;
+    hipLaunchKernelGGL(kern, dim3(bulk), dim3(256), 0, st, (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a,
+                       g.scales_b, (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tiles_m, tiles_n,
+                       kGroupM, 0, -1, residual_args(g), nullptr, 1);
   }
   if (rem > 0) {
     if (sub_log2 == 2) {
-      hipLaunchKernelGGL((fp8_gemm_4w<kBf16, kEpi, 128, 128, S>), dim3(rem << 2), dim3(256), 0, st,
-                         (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a, g.scales_b,
-                         (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tiles_m,
-                         tiles_n, kGroupM, bulk, 2, residual_args(g));
+      auto kern = fp8_gemm_4w<kBf16, kEpi, 128, 128, D>;
+      hipLaunchKernelGGL(kern, dim3(rem << 2), dim3(256), 0, st, (const uint8_t*)g.A, (const uint8_t*)g.W,
+                         g.scales_a, g.scales_b, (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N, g.K, g.ldc,
+                         tiles_m, tiles_n, kGroupM, bulk, 2, residual_args(g), nullptr, 1);
     } else {
-      hipLaunchKernelGGL((fp8_gemm_4w<kBf16, kEpi, 256, 128, S>), dim3(rem << 1), dim3(256), 0, st,
-                         (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a, g.scales_b,
-                         (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tiles_m,
-                         tiles_n, kGroupM, bulk, 1, residual_args(g));
+      auto kern = fp8_gemm_4w<kBf16, kEpi, 256, 128, D>;
+      hipLaunchKernelGGL(kern, dim3(rem << 1), dim3(256), 0, st, (const uint8_t*)g.A, (const uint8_t*)g.W,
+                         g.scales_a, g.scales_b, (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N, g.K, g.ldc,
+                         tiles_m, tiles_n, kGroupM, bulk, 1, residual_args(g), nullptr, 1);
     }
   }
   return hipGetLastError();
 }
 
-// Small M (<= 256 rows): one launch of BM x BN tiles, no 256x256 macro tiles.
-// M <= 64: 64x64 tiles. Otherwise 128x64 if its tiles fit one round of the CUs,
-// else 128x128 (fewer, larger tiles). Measured on MI355X with W read from HBM
-// (M x N, K 5120): 64 x 15360: 64x64 27.8 us vs 29.3 (128x64) and 36.8 (128x128);
-// 256 x 15360: 128x128 40.3 us vs 55.5 (128x64); 256 x 5120: 128x64 29.4 us vs
-// 36.1 (128x128) and 36.0 (64x64). Deeper operand rings (up to 16 stages) and
-// staggered K starts did not change these times.
-constexpr int kSmallMaxM = 256;
-
-template <bool kBf16, int kEpi, int BM, int BN, int S>
+// Fallback for small M when K is not a multiple of 128 (64-byte K steps, one launch):
+// M <= 64: 64x64 tiles; otherwise 128x64 if its tiles fit one round of the CUs, else
+// 128x128.
+template <bool kBf16, int kEpi, int BM, int BN, int D>
 hipError_t launch_direct(const GemmArgs& g, hipStream_t st) {
   const int tiles_m = (g.M + BM - 1) / BM, tiles_n = (g.N + BN - 1) / BN;
-  hipLaunchKernelGGL((fp8_gemm_4w<kBf16, kEpi, BM, BN, S>), dim3(tiles_m * tiles_n), dim3(256), 0, st,
-                     (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias,
-                     (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tiles_m, tiles_n, 1, 0, -2, residual_args(g));
+  auto kern = fp8_gemm_4w<kBf16, kEpi, BM, BN, D>;
+  hipLaunchKernelGGL(kern, dim3(tiles_m * tiles_n), dim3(256), 0, st, (const uint8_t*)g.A, (const uint8_t*)g.W,
+                     g.scales_a, g.scales_b, (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tiles_m,
+                     tiles_n, 1, 0, -2, residual_args(g), nullptr, 1);
   return hipGetLastError();
+}
+
+// Split-K reduction and epilogue: thread t owns 8 consecutive columns of one row,
+// sums the splits' fp32 partials in split order (so the result does not depend on
+// which block finished first), then applies the epilogue of store_tile_lds.
+template <bool kBf16, int kEpi>
+__global__ __launch_bounds__(256) void fp8_gemm_splitk_reduce(
+    const float* __restrict__ ws, int splits, const float* __restrict__ sa, const float* __restrict__ sb,
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ C, int M, int N, int64_t ldc,
+    ResidualArgs res) {
+  const int groups = N >> 3;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= (int64_t)M * groups) return;
+  const int m = (int)(t / groups), n = (int)(t - (int64_t)m * groups) * 8;
+  const int64_t split_stride = (int64_t)M * N;
+  const float* p = ws + (int64_t)m * N + n;
+  float acc[8];
+  {
+    const float4 a = *(const float4*)p, b = *(const float4*)(p + 4);
+    acc[0] = a.x; acc[1] = a.y; acc[2] = a.z; acc[3] = a.w;
+    acc[4] = b.x; acc[5] = b.y; acc[6] = b.z; acc[7] = b.w;
+  }
+#pragma unroll 4
+  for (int s = 1; s < splits; ++s) {
+    const float* q = p + s * split_stride;
+    const float4 a = *(const float4*)q, b = *(const float4*)(q + 4);
+    acc[0] += a.x; acc[1] += a.y; acc[2] += a.z; acc[3] += a.w;
+    acc[4] += b.x; acc[5] += b.y; acc[6] += b.z; acc[7] += b.w;
+  }
+  const float s_a = sa[m];
+  const float4 sb0 = *(const float4*)(sb + n), sb1 = *(const float4*)(sb + n + 4);
+  const float sbe[8] = {sb0.x, sb0.y, sb0.z, sb0.w, sb1.x, sb1.y, sb1.z, sb1.w};
+  float be[8];
+  if (bias) {
+    const uint4 bb = *(const uint4*)(bias + n);
+    const uint32_t w[4] = {bb.x, bb.y, bb.z, bb.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      be[2 * e] = unpack_lo<kBf16>(w[e]);
+      be[2 * e + 1] = unpack_hi<kBf16>(w[e]);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) be[e] = 0.0f;
+  }
+  uint32_t pk[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    pk[e] = pack2<kBf16>(__builtin_fmaf(acc[2 * e] * sbe[2 * e], s_a, be[2 * e]),
+                         __builtin_fmaf(acc[2 * e + 1] * sbe[2 * e + 1], s_a, be[2 * e + 1]));
+    if constexpr (kEpi == kEpiGelu)
+      pk[e] = pack2<kBf16>(gelu_tanh(unpack_lo<kBf16>(pk[e])), gelu_tanh(unpack_hi<kBf16>(pk[e])));
+  }
+  uint4 v = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+  if constexpr (kEpi == kEpiResidual) {
+    const uint4 gv = *(const uint4*)(res.gate + n);
+    const uint4 x = *(const uint4*)(res.ptr + (int64_t)m * res.ld + n);
+    v = make_uint4(gated_pair<kBf16>(v.x, x.x, gv.x), gated_pair<kBf16>(v.y, x.y, gv.y),
+                   gated_pair<kBf16>(v.z, x.z, gv.z), gated_pair<kBf16>(v.w, x.w, gv.w));
+  }
+  *(uint4*)(C + (int64_t)m * ldc + n) = v;
+}
+
+// Deep-K launch of BM x BN tiles: one launch (splits == 1) or a split-K partial
+// launch plus the reduce (splits > 1; ws holds splits * M * N floats).
+template <bool kBf16, int kEpi, int BM, int BN, int KS, int U>
+hipError_t launch_deepk(const GemmArgs& g, int splits, float* ws, hipStream_t st) {
+  const int tiles_m = (g.M + BM - 1) / BM, tiles_n = (g.N + BN - 1) / BN;
+  if (splits <= 1) {
+    hipLaunchKernelGGL((fp8_gemm_4k<kBf16, kEpi, BM, BN, KS, U>), dim3(tiles_m * tiles_n), dim3(256), 0, st,
+                       (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias,
+                       (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tiles_m, tiles_n, 1, 0, -2, residual_args(g), nullptr, 1);
+    return hipGetLastError();
+  }
+  hipLaunchKernelGGL((fp8_gemm_4k<true, kEpiPartial, BM, BN, KS, U>), dim3(tiles_m * tiles_n * splits), dim3(256), 0,
+                     st, (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias,
+                     (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tiles_m, tiles_n, 1, 0, -3, residual_args(g), ws, splits);
+  const int64_t threads = (int64_t)g.M * (g.N / 8);
+  hipLaunchKernelGGL((fp8_gemm_splitk_reduce<kBf16, kEpi>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                     st, ws, splits, g.scales_a, g.scales_b, (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N,
+                     g.ldc, residual_args(g));
+  return hipGetLastError();
+}
+
+// Small M (<= 512 rows): deep-K tiles (fp8_gemm_4k), split over K where the tiles
+// alone would leave most CUs idle (splits = CUs / tiles, rounded, at most 8 and at
+// least 4 K steps per split). Measured on MI355X with W read from HBM, K 5120 unless
+// stated (the reference's hipBLASLt GEMM, torch._scaled_mm, on the same inputs in
+// brackets; the 64-byte-step kernel before it in braces):
+//   M 64:  64x64 tiles, 256-byte K steps, 3 staging buffers:
+//          N 15360: 20.9 us (20.5) {28.4};  N 5120, 3 splits: 12.4 us (15.3) {23.9}
+//   M 256: 128x128 tiles, 128-byte K steps:
+//          N 15360: 41.3 us (40.3) {42.1};  N 5120, 3 splits: 22.4 us (30.8) {28.1}
+//   M 512: 128x256 tiles, 128-byte K steps:
+//          N 15360: 62.0 us (53.0) {62.2};  N 5120, 3 splits: 33.8 us (31.6) {35.7};
+//          K 13824, N 5120, 3 splits: 59.6 us {80.9}
+constexpr int kSmallMaxM = 512;
+
+struct SmallPlan {
+  int kind;  // 0: no deep-K plan for this shape; 1: 64x64/256 B; 2: 128x128/128 B; 3: 128x256/128 B
+  int splits;
+};
+
+SmallPlan small_plan(int M, int N, int K) {
+  int bm, bn, ks, kind;
+  if (M > kSmallMaxM || M <= 0 || N <= 0) return SmallPlan{0, 1};
+  if (M <= 64) {
+    kind = 1, bm = 64, bn = 64, ks = 256;
+  } else if (M <= 256) {
+    kind = 2, bm = 128, bn = 128, ks = 128;
+  } else {
+    kind = 3, bm = 128, bn = 256, ks = 128;
+  }
+  if (K % ks != 0) return SmallPlan{0, 1};
+  const int tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+  int s = (device_cus() + tiles / 2) / tiles;
+  s = min(s, max(1, (K / ks) / 4));
+  s = max(1, min(s, 8));
+  return SmallPlan{kind, s};
 }
 
 template <bool kBf16, int kEpi>
 hipError_t launch_small_m(const GemmArgs& g, hipStream_t st) {
+  SmallPlan p = small_plan(g.M, g.N, g.K);
+  if (p.splits > 1 && (g.workspace == nullptr || g.workspace_bytes < (int64_t)p.splits * g.M * g.N * 4))
+    p.splits = 1;  // no (or too small a) workspace: the same tiles in one launch
+  float* ws = (float*)g.workspace;
+  switch (p.kind) {
+    case 1:
+      return launch_deepk<kBf16, kEpi, 64, 64, 256, 3>(g, p.splits, ws, st);
+    case 2:
+      return launch_deepk<kBf16, kEpi, 128, 128, 128, 2>(g, p.splits, ws, st);
+    case 3:
+      return launch_deepk<kBf16, kEpi, 128, 256, 128, 2>(g, p.splits, ws, st);
+    default:
+      break;
+  }
+  if (g.M > 256) return launch_4w<kBf16, kEpi>(g, st);
   if (g.M <= 64) return launch_direct<kBf16, kEpi, 64, 64, 8>(g, st);
   const int64_t tiles_128x64 = (int64_t)((g.M + 127) / 128) * ((g.N + 63) / 64);
   if (tiles_128x64 <= device_cus()) return launch_direct<kBf16, kEpi, 128, 64, 6>(g, st);
@@ -604,6 +968,12 @@ hipError_t launch_gemm_t(const GemmArgs& g, hipStream_t st) {
 }
 
 }  // namespace
+
+int64_t fp8_gemm_workspace_bytes(int M, int N, int K) {
+  if (K < 64 || K % 64 != 0 || N % 8 != 0) return 0;
+  const SmallPlan p = small_plan(M, N, K);
+  return p.splits > 1 ? (int64_t)p.splits * M * N * 4 : 0;
+}
 
 hipError_t launch_fp8_gemm(const GemmArgs& g, hipStream_t st) {
   if (g.M == 0 || g.N == 0) return hipSuccess;

@@ -48,6 +48,10 @@ struct GemmArgs {
   const void* residual;  // [M, N] of out dtype, row stride ldr (may equal C with ldr == ldc)
   int64_t ldr;
   const void* gate;  // [N] of out dtype
+  // split-K workspace (16-byte aligned) or null; used when workspace_bytes covers
+  // fp8_gemm_workspace_bytes(M, N, K)
+  void* workspace;
+  int64_t workspace_bytes;
 };
 
 // bf16 [len, H, D] view: element (t, h, d) at ptr[t * stride_token + h * stride_head + d].
@@ -104,6 +108,8 @@ hipError_t launch_per_token_quant(const void* in, bool in_fp16, void* q, float* 
                                   int64_t K, bool divide, hipStream_t st);
 hipError_t launch_qk_norm_rope(const NormRopeArgs& a, int head_dim, hipStream_t st);
 hipError_t launch_fp8_gemm(const GemmArgs& g, hipStream_t st);
+// Workspace bytes the GEMM of this shape can use on the current device (0: none).
+int64_t fp8_gemm_workspace_bytes(int M, int N, int K);
 hipError_t launch_norm_modulate(const NormModArgs& a, hipStream_t st);
 hipError_t launch_joint_qkv_pack(const JointPackArgs& a, hipStream_t st);
 hipError_t launch_cached_kv_pack(const CachedPackArgs& a, hipStream_t st);

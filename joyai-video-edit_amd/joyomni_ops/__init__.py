@@ -201,13 +201,23 @@ def _scaled_mm_checks(mat_a, mat_b, scales_a, scales_b, out_dtype, bias):
     return M, N, K
 
 
+def _gemm_workspace(M, N, K, device):
+    """Split-K workspace of the small-M GEMM plans (None when the shape uses none); allocated
+    from torch's caching allocator like the output, so a captured graph keeps its own."""
+    nbytes = _LIB.joy_fp8_scaled_mm_workspace_size(M, N, K)
+    if nbytes <= 0:
+        return None, 0
+    return torch.empty(nbytes, dtype=torch.uint8, device=device), nbytes
+
+
 def _scaled_mm_impl(mat_a, mat_b, scales_a, scales_b, out_dtype, bias, epilogue):
     M, N, K = _scaled_mm_checks(mat_a, mat_b, scales_a, scales_b, out_dtype, bias)
     out = torch.empty((M, N), device=mat_a.device, dtype=out_dtype)
     with torch.cuda.device(mat_a.device):
+        ws, ws_bytes = _gemm_workspace(M, N, K, mat_a.device)
         st = _LIB.joy_fp8_scaled_mm(
             _ptr(mat_a), _ptr(mat_b), _ptr(scales_a), _ptr(scales_b), _ptr(bias), _ptr(out),
-            _OUT_CODE[out_dtype], M, N, K, epilogue, _stream(mat_a))
+            _OUT_CODE[out_dtype], M, N, K, epilogue, _ptr(ws), ws_bytes, _stream(mat_a))
     _lib.check(_LIB, st)
     return out
 
@@ -238,9 +248,10 @@ def _gated_residual_impl(mat_a, mat_b, scales_a, scales_b, residual, gate, bias,
         gate = gate.clone(memory_format=torch.contiguous_format)  # N values: a 16-byte aligned copy
     ld = residual.stride(0) if M > 1 else N
     with torch.cuda.device(mat_a.device):
+        ws, ws_bytes = _gemm_workspace(M, N, K, mat_a.device)
         st = _LIB.joy_fp8_scaled_mm_gated_residual(
             _ptr(mat_a), _ptr(mat_b), _ptr(scales_a), _ptr(scales_b), _ptr(bias), _ptr(residual), ld,
-            _ptr(gate), _ptr(out), _OUT_CODE[out_dtype], M, N, K, _stream(mat_a))
+            _ptr(gate), _ptr(out), _OUT_CODE[out_dtype], M, N, K, _ptr(ws), ws_bytes, _stream(mat_a))
     _lib.check(_LIB, st)
 
 

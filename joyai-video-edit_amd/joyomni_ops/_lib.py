@@ -48,9 +48,10 @@ SIGNATURES = {
     "joy_abi_version": (_int, []),
     "joy_last_error": (ctypes.c_char_p, []),
     "joy_per_token_quant_fp8": (_int, [_vp, _int, _vp, _vp, _i64, _i64, _int, _vp]),
-    "joy_fp8_scaled_mm": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _int, _i64, _i64, _i64, _int, _vp]),
+    "joy_fp8_scaled_mm": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _int, _i64, _i64, _i64, _int, _vp, _i64, _vp]),
+    "joy_fp8_scaled_mm_workspace_size": (_i64, [_i64, _i64, _i64]),
     "joy_fp8_scaled_mm_gated_residual": (
-        _int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _int, _i64, _i64, _i64, _vp]),
+        _int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _int, _i64, _i64, _i64, _vp, _i64, _vp]),
     "joy_fused_qk_norm_rope_3d_paired": (
         _int, [_vp, _vp, _i64, _i64, _i64, _i64, _f32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "joy_fused_qkv_norm_rope_cache": (
@@ -70,7 +71,7 @@ SIGNATURES = {
                _vp]),
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 
 class JoyError(RuntimeError):

@@ -61,19 +61,36 @@ def test_quant_argument_checks(lib):
 def test_gemm_argument_checks(lib):
     p = ctypes.c_void_p(0x1000)
     args = lambda **kw: [kw.get("a", p), kw.get("b", p), p, p, None, p, kw.get("dt", 0),  # noqa: E731
-                         kw.get("M", 64), kw.get("N", 64), kw.get("K", 64), kw.get("epi", 0), None]
+                         kw.get("M", 64), kw.get("N", 64), kw.get("K", 64), kw.get("epi", 0),
+                         kw.get("ws", None), kw.get("wsb", 0), None]
     _status(lib, lib.joy_fp8_scaled_mm(*args(K=40)), 1, "multiple of 16 bytes")
     _status(lib, lib.joy_fp8_scaled_mm(*args(N=36)), 1, "out must be multiple of 16 bytes")
     _status(lib, lib.joy_fp8_scaled_mm(*args(dt=5)), 1, "Half or BFloat16")
     _status(lib, lib.joy_fp8_scaled_mm(*args(epi=9)), 1, "epilogue")
     _status(lib, lib.joy_fp8_scaled_mm(*args(a=ctypes.c_void_p(0x1008))), 2, "16-byte aligned")
+    _status(lib, lib.joy_fp8_scaled_mm(*args(wsb=-1)), 1, "workspace_bytes")
+    _status(lib, lib.joy_fp8_scaled_mm(*args(wsb=4096)), 1, "with a workspace")
+    _status(lib, lib.joy_fp8_scaled_mm(*args(ws=ctypes.c_void_p(0x1004), wsb=4096)), 1,
+            "workspace must be 16-byte aligned")
     assert lib.joy_fp8_scaled_mm(*args(M=0)) == 0
+
+
+def test_gemm_workspace_size(lib):
+    """Host-side plan: split-K only for small M where the tiles leave CUs idle (256-CU MI355X
+    when no device is visible); the size is splits * M * N fp32 partial sums."""
+    size = lib.joy_fp8_scaled_mm_workspace_size
+    ws = size(64, 5120, 5120)
+    assert ws > 0 and ws % (64 * 5120 * 4) == 0 and 2 <= ws // (64 * 5120 * 4) <= 8
+    assert size(10800, 5120, 5120) == 0      # large M: full rounds of 256x256 tiles, no split
+    assert size(64, 15360, 5120) == 0        # 240 tiles already cover the CUs
+    assert size(64, 5120, 5120 + 64) == 0    # K not a multiple of the plan's K step
+    assert size(0, 5120, 5120) == 0 and size(-1, 8, 64) == 0 and size(64, 36, 64) == 0
 
 
 def test_gated_residual_argument_checks(lib):
     p, r, g = ctypes.c_void_p(0x1000), ctypes.c_void_p(0x2000), ctypes.c_void_p(0x3000)
     args = lambda **kw: [p, p, p, p, None, kw.get("r", r), kw.get("ld", 64), kw.get("g", g),  # noqa: E731
-                         kw.get("out", p), 0, kw.get("M", 64), 64, 64, None]
+                         kw.get("out", p), 0, kw.get("M", 64), 64, 64, None, 0, None]
     f = lib.joy_fp8_scaled_mm_gated_residual
     _status(lib, f(*args(r=None)), 1, "residual must be non-null")
     _status(lib, f(*args(g=None)), 1, "gate must be non-null")

@@ -41,7 +41,9 @@ def operands(qa, qw, sa, sw):
 
 
 @pytest.mark.parametrize("M,N,K", [(300, 264, 256), (1, 520, 384), (200, 4104, 640), (33, 40, 48),
-                                   (513, 520, 384)])
+                                   (513, 520, 384),
+                                   # small-M plans with a K split (partials reduced before the epilogue)
+                                   (64, 2048, 4096), (500, 4104, 1664)])
 def test_exact_problems_bit_exact(M, N, K):
     import joyomni_ops as jo
     announce("gated residual exact", M, N, K)

@@ -169,6 +169,87 @@ def test_cfg3_small_m(M, N):
     assert_tolerance(y, ref, f"cfg3 M={M} N={N}")
 
 
+def gemm_capi(qa_u8, qw_u8, sa, sw, bias_u16, out_dtype, workspace):
+    """joy_fp8_scaled_mm through the C ABI with an explicit workspace choice."""
+    import joyomni_ops as jo
+    from joyomni_ops import _lib
+    M, K = qa_u8.shape
+    N = qw_u8.shape[0]
+    a, w = to_dev_fp8(qa_u8), to_dev_fp8(qw_u8)
+    sa_d = torch.from_numpy(sa).to(DEV)
+    sw_d = torch.from_numpy(sw).to(DEV)
+    b = torch.from_numpy(bias_u16.view(np.int16)).view(out_dtype).to(DEV)
+    out = torch.empty(M, N, dtype=out_dtype, device=DEV)
+    ws_bytes = jo._LIB.joy_fp8_scaled_mm_workspace_size(M, N, K)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=DEV) if workspace else None
+    st = jo._LIB.joy_fp8_scaled_mm(a.data_ptr(), w.data_ptr(), sa_d.data_ptr(), sw_d.data_ptr(), b.data_ptr(),
+                                   out.data_ptr(), 0 if out_dtype == torch.bfloat16 else 1, M, N, K, 0,
+                                   ws.data_ptr() if ws is not None else None, ws_bytes if workspace else 0,
+                                   torch.cuda.current_stream().cuda_stream)
+    _lib.check(jo._LIB, st)
+    torch.cuda.synchronize()
+    return out, ws_bytes
+
+
+# Small-M plans (64-row tiles with 256-byte K steps for M <= 64, 128x128 / 128x256 tiles with
+# 128-byte K steps up to M = 512), each with and without a K split: ragged rows, partial
+# column tiles, uneven split ranges, and the block's 512-token FFN-down shape.
+SMALL_M_PLAN_SHAPES = [(64, 5120, 5120), (33, 1032, 4096), (1, 264, 2048), (64, 15360, 256),
+                       (200, 2056, 2048), (256, 5120, 1280), (129, 4104, 3072),
+                       (500, 4104, 1664), (512, 5120, 13824), (320, 15360, 512)]
+
+
+@pytest.mark.parametrize("M,N,K", SMALL_M_PLAN_SHAPES)
+def test_small_m_plans_exact_with_and_without_workspace(M, N, K):
+    """Exact small integers fix every output bit whatever the split: the torch op (workspace
+    allocated), the C ABI with the workspace and the C ABI without it (same tiles, no split)
+    must all equal the oracle."""
+    announce("gemm small-M plan", M, N, K)
+    rng = np.random.default_rng(M * 13 + N + K)
+    qa = f32_to_e4m3fn(rng.integers(-8, 9, (M, K)).astype(np.float32))
+    qw = f32_to_e4m3fn(rng.integers(-8, 9, (N, K)).astype(np.float32))
+    sa = (2.0 ** rng.integers(-12, -4, M)).astype(np.float32)
+    sw = (2.0 ** rng.integers(-12, -4, N)).astype(np.float32)
+    bias = f32_to_bf16((rng.integers(-64, 64, N) / 16).astype(np.float32))
+    exp_bits, _ = og.scaled_mm(qa, qw, sa, sw, bias)
+    assert np.array_equal(u16(gemm(qa, qw, sa, sw, bias)), exp_bits)
+    y_ws, ws_bytes = gemm_capi(qa, qw, sa, sw, bias, torch.bfloat16, True)
+    assert np.array_equal(u16(y_ws), exp_bits)
+    y_nows, _ = gemm_capi(qa, qw, sa, sw, bias, torch.bfloat16, False)
+    assert np.array_equal(u16(y_nows), exp_bits)
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 5120, 5120), (256, 5120, 5120), (512, 5120, 13824)])
+def test_small_m_split_random_within_tolerance(M, N, K):
+    """cfg-0 distributions through a split plan: BASELINE tolerance and the accumulation bound,
+    and the split and unsplit launches agree to the same bound."""
+    announce("gemm small-M split random", M, N, K)
+    qa, sa, qw, sw, bias = quantized_problem(M, N, K, M + N + K)
+    y, ws_bytes = gemm_capi(qa, qw, sa, sw, bias, torch.bfloat16, True)
+    assert ws_bytes > 0, "shape expected to use a K split"
+    y = u16(y)
+    assert_tolerance(y, og.reference_fp32(qa, qw, sa, sw, bias), f"split {M}x{N}x{K}")
+    assert_acc_bound(y, qa, qw, sa, sw, bias, f"split {M}x{N}x{K}")
+    y1 = u16(gemm_capi(qa, qw, sa, sw, bias, torch.bfloat16, False)[0])
+    assert_acc_bound(y1, qa, qw, sa, sw, bias, f"unsplit {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,N,K", [(200, 520, 512), (64, 2048, 4096), (300, 2560, 5120)])
+def test_gelu_epilogue_and_fp16_out_plans(out_dtype, M, N, K):
+    """GELU-tanh on the rounded output, on unsplit and split small-M plans."""
+    announce("gemm gelu plan", out_dtype, M, N, K)
+    qa, sa, qw, sw, bias = quantized_problem(M, N, K, 11 + M)
+    bias_t = torch.from_numpy(bf16_to_f32(bias)).to(out_dtype)
+    bias_bits = bias_t.view(torch.int16).numpy().view(np.uint16)
+    plain = gemm(qa, qw, sa, sw, bias_bits, out_dtype)
+    gel = gemm(qa, qw, sa, sw, bias_bits, out_dtype, gelu=True)
+    ref = torch.nn.functional.gelu(plain.float(), approximate="tanh").to(out_dtype)
+    diff = (gel.float() - ref.float()).abs()
+    tol = (ref.float().abs() * (2.0 ** -7 if out_dtype == torch.bfloat16 else 2.0 ** -10)).clamp_min(1e-6)
+    assert bool((diff <= tol).all()), float((diff - tol).max())
+
+
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
 def test_gelu_epilogue_and_fp16_out(out_dtype):
     announce("gemm gelu", out_dtype)
