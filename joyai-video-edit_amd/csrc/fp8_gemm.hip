@@ -601,24 +601,44 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
+// Instruction interleave of one deep-K iteration: N MFMAs with the R fragment reads
+// spread over all of them, the L global loads after the first L MFMAs and the L
+// LDS writes after the last L.
+template <int I, int N, int R, int L>
+__device__ __forceinline__ void sched_pattern_k() {
+  if constexpr (I < N) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+    constexpr int RD = (R + N - 1) / N;
+    if constexpr (I * RD < R) __builtin_amdgcn_sched_group_barrier(0x100, RD, 0);  // LDS reads
+    if constexpr (I < L) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);        // one global load
+    if constexpr (I >= N - L) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);   // one LDS write
+    sched_pattern_k<I + 1, N, R, L>();
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Deep-K register-staged kernel for grids of at most a few rounds (small M): the
 // tiles, waves, MFMA fragments, launch modes and epilogue of fp8_gemm_4w, with K
 // steps of KS = 128..512 bytes so that each barrier covers KS/64 MFMA k-steps and
-// each load instruction reads whole 256..512-byte row runs. Small-M GEMMs are
-// bound by the bytes each CU keeps in flight against ~2 us of loaded memory
-// latency; a 64x64 tile with KS = 512 keeps 64 KB per step and block in flight.
+// each load instruction reads whole 256..512-byte row runs, and with operands
+// going global -> VGPR -> LDS (16-byte loads, 1 KB-contiguous LDS writes). Small-M
+// GEMMs are bound by the bytes each CU keeps in flight against ~2 us of loaded
+// memory latency, which deep steps and register staging raise; the 64-byte-step
+// DMA kernel streams W at under 3 TB/s on these shapes.
 //
-// LDS holds two slots of one K step; U staging buffers of one step live in VGPRs.
-// Iteration t (after one barrier):
-//   * loads step t+U into staging buffer t % U (its previous step t was written
-//     to LDS in iteration t-1),
-//   * runs the MFMAs of step t from slot t % 2, reading the fragments of k-step
-//     s+1 while the MFMAs of k-step s run,
-//   * writes step t+1 (loaded U-1 iterations earlier) into slot (t+1) % 2, which
-//     every wave finished reading in iteration t-1, before this iteration's barrier.
+// U staging buffers of one K step live in VGPRs (step j in buffer j % U); LDS holds
+// NS slots of one step (step j in slot j % NS), and steps are written AHEAD = NS - 1
+// iterations before they are used. Iteration t (after one barrier):
+//   * loads step t+AHEAD+U-1 into its staging buffer (that buffer's previous step,
+//     t+AHEAD-1, was written to LDS in iteration t-1),
+//   * runs the MFMAs of step t, reading the fragments of k-step s+1 while the MFMAs
+//     of k-step s run,
+//   * writes step t+AHEAD into slot (t+AHEAD) % NS = (t-1) % NS: step t-1's slot,
+//     whose reads every wave completed before this iteration's barrier.
+// With NS = 3 step t+1 (written in iteration t-1) is already visible, so the
+// fragments of its first k-step are read during step t's last MFMAs.
 // ---------------------------------------------------------------------------
-template <bool kBf16, int kEpi, int BM, int BN, int KS, int U>
+template <bool kBf16, int kEpi, int BM, int BN, int KS, int U, int NS>
 __global__ __launch_bounds__(256, 1) void fp8_gemm_4k(
     const uint8_t* __restrict__ A, const uint8_t* __restrict__ W, const float* __restrict__ sa,
     const float* __restrict__ sb, const uint16_t* __restrict__ bias, uint16_t* __restrict__ C,
@@ -632,12 +652,17 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4k(
   constexpr int A_BYTES = BM * KS, SLOT = (BM + BN) * KS;
   constexpr int LOADS = IA + IW;
   constexpr int SUBS = KS / 64;
-  constexpr int UNR = U % 2 == 0 ? U : 2 * U;
+  constexpr int NMFMA = FM * FN, NREAD = 2 * (FM + FN);
+  constexpr int AHEAD = NS - 1;
+  constexpr int UNR = U % NS == 0 ? U : U * NS;  // lcm(U, NS) for NS in {2, 3}
   static_assert(KS >= 128 && KS <= 512, "deep K steps only");
+  static_assert(NS == 2 || NS == 3, "two or three LDS slots");
   static_assert(U >= 2, "at least two staging buffers");
+  static_assert(UNR % U == 0 && UNR % NS == 0, "buffer and slot indices compile-time in the unrolled loop");
   static_assert(IA * RPI * NW == BM && IW * RPI * NW == BN, "tile rows must split over waves");
   constexpr int STAGE_BYTES = WTM * (WTN * 2 + 16);
-  constexpr int LDS_BYTES = 2 * SLOT > NW * STAGE_BYTES ? 2 * SLOT : NW * STAGE_BYTES;
+  constexpr int LDS_BYTES = NS * SLOT > NW * STAGE_BYTES ? NS * SLOT : NW * STAGE_BYTES;
+  static_assert(LDS_BYTES <= 160 * 1024, "LDS of one CU");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
 
   const int lane = threadIdx.x & 63;
@@ -678,7 +703,7 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4k(
     for (int j = 0; j < FM; ++j) acc[i][j] = (v16f){};
 
   v8i fw[2][FN], fa[2][FM];
-  // fragments of k-step ks (64 bytes: logical chunks 4 ks + 2 g and + 1) of the step in `slot`
+  // fragments of k-step KK (64 bytes: logical chunks 4 KK + 2 g and + 1) of the step in `slot`
   auto read_frags = [&](auto sc, auto kc, int slot) {
     constexpr int SL = decltype(sc)::value, KK = decltype(kc)::value;
     const uint8_t* base = lds + slot * SLOT;
@@ -705,25 +730,41 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4k(
 #pragma unroll
       for (int j = 0; j < FM; ++j) acc[i][j] = mfma_32x32x64_fp8(fw[SL][i], fa[SL][j], acc[i][j]);
   };
+  // k-step KK of a step uses fragment set KK % 2 (SUBS is even, so a step starts in set 0)
   auto iteration = [&](auto jc, int t) {
     constexpr int J = decltype(jc)::value;
-    constexpr int CUR = J & 1;
+    constexpr int CUR = J % NS, NXT = (J + 1) % NS, WRT = (J + AHEAD) % NS;
+    __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): own LDS writes and fragment reads done
     block_barrier();
-    gload(IC<J % U>{}, t + U);
-    read_frags(IC<0>{}, IC<0>{}, CUR);
-    static_for<1, SUBS>([&](auto kc) {
+    __builtin_amdgcn_sched_barrier(0);
+    gload(IC<(J + AHEAD - 1) % U>{}, t + AHEAD + U - 1);
+    if constexpr (NS == 2) read_frags(IC<0>{}, IC<0>{}, CUR);
+    static_for<0, SUBS>([&](auto kc) {
       constexpr int KK = decltype(kc)::value;
-      read_frags(IC<KK & 1>{}, kc, CUR);
-      mfmas(IC<(KK - 1) & 1>{});
+      if constexpr (KK + 1 < SUBS) {
+        read_frags(IC<(KK + 1) & 1>{}, IC<KK + 1>{}, CUR);
+      } else if constexpr (NS == 3) {
+        read_frags(IC<0>{}, IC<0>{}, NXT);  // first k-step of step t+1
+      }
+      mfmas(IC<KK & 1>{});
     });
-    mfmas(IC<(SUBS - 1) & 1>{});
-    lwrite(IC<(J + 1) % U>{}, CUR ^ 1);
+    lwrite(IC<(J + AHEAD) % U>{}, WRT);
+    sched_pattern_k<0, NMFMA * SUBS, NREAD * SUBS, LOADS>();
+    __builtin_amdgcn_sched_barrier(0);
   };
 
-  // prologue: steps 0..U-1 into the staging buffers, step 0 into slot 0
+  // prologue: steps 0..U-1 into the staging buffers, steps 0..AHEAD-1 into their slots,
+  // steps U..U+AHEAD-2 into the freed buffers; with three slots, the first k-step of
+  // step 0 into registers
   static_for<0, U>([&](auto bc) { gload(bc, decltype(bc)::value); });
-  lwrite(IC<0>{}, 0);
+  static_for<0, AHEAD>([&](auto bc) { lwrite(bc, decltype(bc)::value); });
+  static_for<0, AHEAD - 1>([&](auto bc) { gload(bc, U + decltype(bc)::value); });
+  if constexpr (NS == 3) {
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    block_barrier();
+    read_frags(IC<0>{}, IC<0>{}, 0);
+  }
 
   int kt = 0;
   for (; kt + UNR <= nk; kt += UNR) static_for<0, UNR>([&](auto jc) { iteration(jc, kt + decltype(jc)::value); });
@@ -868,16 +909,16 @@ __global__ __launch_bounds__(256) void fp8_gemm_splitk_reduce(
 
 // Deep-K launch of BM x BN tiles: one launch (splits == 1) or a split-K partial
 // launch plus the reduce (splits > 1; ws holds splits * M * N floats).
-template <bool kBf16, int kEpi, int BM, int BN, int KS, int U>
+template <bool kBf16, int kEpi, int BM, int BN, int KS, int U, int NS>
 hipError_t launch_deepk(const GemmArgs& g, int splits, float* ws, hipStream_t st) {
   const int tiles_m = (g.M + BM - 1) / BM, tiles_n = (g.N + BN - 1) / BN;
   if (splits <= 1) {
-    hipLaunchKernelGGL((fp8_gemm_4k<kBf16, kEpi, BM, BN, KS, U>), dim3(tiles_m * tiles_n), dim3(256), 0, st,
+    hipLaunchKernelGGL((fp8_gemm_4k<kBf16, kEpi, BM, BN, KS, U, NS>), dim3(tiles_m * tiles_n), dim3(256), 0, st,
                        (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias,
                        (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tiles_m, tiles_n, 1, 0, -2, residual_args(g), nullptr, 1);
     return hipGetLastError();
   }
-  hipLaunchKernelGGL((fp8_gemm_4k<true, kEpiPartial, BM, BN, KS, U>), dim3(tiles_m * tiles_n * splits), dim3(256), 0,
+  hipLaunchKernelGGL((fp8_gemm_4k<true, kEpiPartial, BM, BN, KS, U, NS>), dim3(tiles_m * tiles_n * splits), dim3(256), 0,
                      st, (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias,
                      (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tiles_m, tiles_n, 1, 0, -3, residual_args(g), ws, splits);
   const int64_t threads = (int64_t)g.M * (g.N / 8);
@@ -888,55 +929,60 @@ hipError_t launch_deepk(const GemmArgs& g, int splits, float* ws, hipStream_t st
 }
 
 // Small M (<= 512 rows): deep-K tiles (fp8_gemm_4k), split over K where the tiles
-// alone would leave most CUs idle (splits = CUs / tiles, rounded, at most 8 and at
-// least 4 K steps per split). Measured on MI355X with W read from HBM, K 5120 unless
-// stated (the reference's hipBLASLt GEMM, torch._scaled_mm, on the same inputs in
-// brackets; the 64-byte-step kernel before it in braces):
-//   M 64:  64x64 tiles, 256-byte K steps, 3 staging buffers:
-//          N 15360: 20.9 us (20.5) {28.4};  N 5120, 3 splits: 12.4 us (15.3) {23.9}
-//   M 256: 128x128 tiles, 128-byte K steps:
-//          N 15360: 41.3 us (40.3) {42.1};  N 5120, 3 splits: 22.4 us (30.8) {28.1}
-//   M 512: 128x256 tiles, 128-byte K steps:
-//          N 15360: 62.0 us (53.0) {62.2};  N 5120, 3 splits: 33.8 us (31.6) {35.7};
-//          K 13824, N 5120, 3 splits: 59.6 us {80.9}
+// alone would leave most CUs idle (splits = CUs / tiles, at most 8 and at least 4 K
+// steps per split). Measured on MI355X with W read from HBM, K 5120 unless stated;
+// the reference's hipBLASLt GEMM (torch._scaled_mm) on the same inputs in brackets,
+// the 64-byte-step DMA kernel in braces:
+//   M 64:  64x64 tiles, 256-byte K steps, 3 staging buffers, 2 LDS slots:
+//          N 15360: 20.9 us (20.4) {28.4};  N 5120, 3 splits: 12.8 us (15.3) {23.9}
+//   M 256: 128x128 tiles, 128-byte K steps, 3 staging buffers, 3 LDS slots:
+//          N 15360: 35.0 us (41.1) {42.1};  N 5120, 3 splits: 21.6 us (30.4) {28.1}
+//   M 512: N 5120: 128x128 as for M 256: 29.5 us (31.2) {35.7}
+//          128x256 tiles, 128-byte K steps, 2 staging buffers, 3 LDS slots, where they
+//          fill 3/4 of the CUs or K is long enough to split:
+//          N 15360: 56.7 us (54.6) {62.2};  N 13824: 53.4 us {58.6};
+//          K 13824, N 5120, 3 splits: 57.2 us {80.9} (128x128 without split: 63.4 us)
 constexpr int kSmallMaxM = 512;
 
 struct SmallPlan {
-  int kind;  // 0: no deep-K plan for this shape; 1: 64x64/256 B; 2: 128x128/128 B; 3: 128x256/128 B
+  int kind;  // 0: no deep-K plan; 1: 64x64 / 256 B steps; 2: 128x128 / 128 B; 3: 128x256 / 128 B
   int splits;
 };
 
-SmallPlan small_plan(int M, int N, int K) {
-  int bm, bn, ks, kind;
+SmallPlan small_plan(int M, int N, int K, bool allow_split) {
   if (M > kSmallMaxM || M <= 0 || N <= 0) return SmallPlan{0, 1};
+  const int P = device_cus();
+  auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+  auto splits_for = [&](int t, int ks) {
+    if (!allow_split) return 1;
+    int s = min(P / t, (K / ks) / 4);
+    return max(1, min(s, 8));
+  };
   if (M <= 64) {
-    kind = 1, bm = 64, bn = 64, ks = 256;
-  } else if (M <= 256) {
-    kind = 2, bm = 128, bn = 128, ks = 128;
-  } else {
-    kind = 3, bm = 128, bn = 256, ks = 128;
+    if (K % 256 != 0) return SmallPlan{0, 1};
+    return SmallPlan{1, splits_for(tiles(64, 64), 256)};
   }
-  if (K % ks != 0) return SmallPlan{0, 1};
-  const int tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
-  int s = (device_cus() + tiles / 2) / tiles;
-  s = min(s, max(1, (K / ks) / 4));
-  s = max(1, min(s, 8));
-  return SmallPlan{kind, s};
+  if (K % 128 != 0) return SmallPlan{0, 1};
+  if (M <= 256) return SmallPlan{2, splits_for(tiles(128, 128), 128)};
+  const int t3 = tiles(128, 256);
+  if (4 * t3 >= 3 * P) return SmallPlan{3, 1};
+  if (K >= 8192 && allow_split) return SmallPlan{3, splits_for(t3, 128)};
+  return SmallPlan{2, splits_for(tiles(128, 128), 128)};
 }
 
 template <bool kBf16, int kEpi>
 hipError_t launch_small_m(const GemmArgs& g, hipStream_t st) {
-  SmallPlan p = small_plan(g.M, g.N, g.K);
+  SmallPlan p = small_plan(g.M, g.N, g.K, true);
   if (p.splits > 1 && (g.workspace == nullptr || g.workspace_bytes < (int64_t)p.splits * g.M * g.N * 4))
-    p.splits = 1;  // no (or too small a) workspace: the same tiles in one launch
+    p = small_plan(g.M, g.N, g.K, false);  // no (or too small a) workspace: best plan without a split
   float* ws = (float*)g.workspace;
   switch (p.kind) {
     case 1:
-      return launch_deepk<kBf16, kEpi, 64, 64, 256, 3>(g, p.splits, ws, st);
+      return launch_deepk<kBf16, kEpi, 64, 64, 256, 3, 2>(g, p.splits, ws, st);
     case 2:
-      return launch_deepk<kBf16, kEpi, 128, 128, 128, 2>(g, p.splits, ws, st);
+      return launch_deepk<kBf16, kEpi, 128, 128, 128, 3, 3>(g, p.splits, ws, st);
     case 3:
-      return launch_deepk<kBf16, kEpi, 128, 256, 128, 2>(g, p.splits, ws, st);
+      return launch_deepk<kBf16, kEpi, 128, 256, 128, 2, 3>(g, p.splits, ws, st);
     default:
       break;
   }
@@ -971,7 +1017,7 @@ hipError_t launch_gemm_t(const GemmArgs& g, hipStream_t st) {
 
 int64_t fp8_gemm_workspace_bytes(int M, int N, int K) {
   if (K < 64 || K % 64 != 0 || N % 8 != 0) return 0;
-  const SmallPlan p = small_plan(M, N, K);
+  const SmallPlan p = small_plan(M, N, K, true);
   return p.splits > 1 ? (int64_t)p.splits * M * N * 4 : 0;
 }
 
