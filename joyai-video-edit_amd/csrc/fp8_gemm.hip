@@ -1004,6 +1004,19 @@ hipError_t launch_gemm_t(const GemmArgs& g, hipStream_t st) {
                     (!g.residual || ((uintptr_t)g.residual % 16 == 0 && g.ldr % 8 == 0 &&
                                      (uintptr_t)g.gate % 16 == 0));
   if (fast && g.M <= kSmallMaxM) return launch_small_m<kBf16, kEpi>(g, st);
+  if (fast && g.M <= 2048 && g.K >= 8192 && g.K % 128 == 0) {
+    // Long K with less than one round of 256x256 tiles (the reference's 16384-wide
+    // FFN-down at 1024 / 1560 tokens): deep-K 128-row tiles. Measured with W from HBM:
+    // 1024 x 16384 x 4096: 79.3 us vs 89.3 (256x256 + split tail); 1560 x 16384 x 4096:
+    // 140.3 us vs 151.7.
+    const int P = device_cus();
+    const int64_t t256 = (int64_t)((g.M + 255) / 256) * ((g.N + 255) / 256);
+    const int64_t t128 = (int64_t)((g.M + 127) / 128) * ((g.N + 127) / 128);
+    if (t256 < P) {
+      if (t128 <= P) return launch_deepk<kBf16, kEpi, 128, 128, 128, 3, 3>(g, 1, nullptr, st);
+      return launch_deepk<kBf16, kEpi, 128, 256, 128, 2, 3>(g, 1, nullptr, st);
+    }
+  }
   if (fast) return launch_4w<kBf16, kEpi>(g, st);
   const int tiles_m = (g.M + 31) / 32, tiles_n = (g.N + 31) / 32;
   const int tiles = tiles_m * tiles_n;
