@@ -26,6 +26,7 @@ sys.path.insert(0, ROOT)
 METRIC = "FP8 GEMM TFLOP/s (% fp8 MFMA peak); QKV-norm-RoPE GB/s (% HBM peak)"
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E, AMD published
 PEAK_FP8_TFLOPS = 5000.0      # MI355X dense FP8 MFMA, AMD published (no sparsity)
+PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA, AMD published (no sparsity)
 
 L_TOK, HEADS, HEAD_DIM = 10800, 40, 128
 E = HEADS * HEAD_DIM
@@ -440,6 +441,33 @@ def bench_block(steps, warmup, n_cached=2):
             "attention_kv_tokens": n_cached * L_TOK + L_TOK + T_COND}
 
 
+def bench_attention(steps, warmup):
+    """The block's joint attention core (dit.py:154-167): video 10800 + condition 512
+    queries over 2 cached chunks + video + condition = 32912 keys, 40 heads x 128, bf16. This
+    build's kernel (joy_attention_fwd, reading the token-major joint operands in place) vs the
+    reference's own call, F.scaled_dot_product_attention on the transposed views (ROCm backend of
+    this torch), on the same inputs; each step one launch, timed with HIP events on the stream."""
+    import torch
+    import joyomni_ops as jo
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(6)
+    Lq, Lk = L_TOK + 512, 3 * L_TOK + 512
+    q = torch.randn(1, Lq, HEADS, HEAD_DIM, generator=g).to(torch.bfloat16).to(dev)
+    k = torch.randn(1, Lk, HEADS, HEAD_DIM, generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn(1, Lk, HEADS, HEAD_DIM, generator=g).to(torch.bfloat16).to(dev)
+    out = torch.empty_like(q)
+    steps_a, warm_a = max(2, min(steps, 10)), max(1, min(warmup, 3))
+    t = time_launches(lambda: jo.sdpa_attention_out(q, k, v, out), steps_a, warm_a)
+    tr = time_launches(lambda: torch.nn.functional.scaled_dot_product_attention(
+        q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), is_causal=False), steps_a, warm_a)
+    flops = 4 * Lq * Lk * HEAD_DIM * HEADS
+    return {"workload": f"joint attention: {Lq} queries x {Lk} keys x {HEADS} heads x {HEAD_DIM}, bf16, "
+                        "non-causal, no mask", "ms": t * 1e3, "tflops": flops / t / 1e12,
+            "frac_bf16_peak": flops / t / 1e12 / PEAK_BF16_TFLOPS,
+            "reference_sdpa_ms": tr * 1e3, "reference_sdpa_tflops": flops / tr / 1e12,
+            "speedup_vs_reference_gpu": tr / t, "steps": steps_a}
+
+
 def bench_copy(steps, warmup):
     """Plain 1 GiB device-to-device copy: the calibration kernel for the
     FETCH_SIZE / WRITE_SIZE counters (known 1 GiB read + 1 GiB write)."""
@@ -509,7 +537,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time plain launches (no HIP graph)")
     ap.add_argument("--only", default="all",
-                    choices=["all", "qkv", "gemm", "refgemm", "small", "quant", "pack", "norm", "block", "copy"])
+                    choices=["all", "qkv", "gemm", "refgemm", "small", "quant", "pack", "norm", "attn", "block", "copy"])
     args = ap.parse_args()
     global EAGER
     EAGER = args.eager
@@ -569,6 +597,10 @@ def main():
     if args.only in ("all", "norm"):
         rec["adaln_norm"] = bench_norm(args.steps, args.warmup)
         progress("adaLN norm done")
+    if args.only in ("all", "attn"):
+        rec["attention_core"] = bench_attention(args.steps, args.warmup)
+        progress(f"attention {rec['attention_core']['ms']:.2f} ms "
+                 f"(torch SDPA {rec['attention_core']['reference_sdpa_ms']:.2f} ms)")
     if args.only in ("all", "block"):
         rec["block_cfg4"] = bench_block(max(3, args.steps // 10), max(1, args.warmup // 5))
         progress(f"cfg4 block {rec['block_cfg4']['block_latency_ms']:.2f} ms")

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define JOY_ABI_VERSION 6
+#define JOY_ABI_VERSION 7
 
 #if defined(__GNUC__) || defined(__clang__)
 #define JOY_API __attribute__((visibility("default")))
@@ -238,6 +238,24 @@ JOY_API joy_status joy_fused_cached_kv_pack(const joy_bf16_view *key0, const joy
                                     const joy_bf16_view *key1, const joy_bf16_view *value1,
                                     const float *cos, const float *sin, int64_t num_heads,
                                     int64_t head_dim, void *out_k, void *out_v, void *stream);
+
+/*
+ * Joint-attention forward (new op): per head, out = softmax(q k^T * scale) v,
+ * non-causal, no mask, bf16 inputs and output, fp32 softmax and accumulation.
+ * Replaces: _sdpa_attention(query, key, value) at deploy/xvideo/models/dit/dit.py:154-167,
+ *   i.e. F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2),
+ *   v.transpose(1, 2), is_causal=False) on bf16 [1, S, H, D] tensors (default scale
+ *   1/sqrt(D)), as called on the joint Q / K / V at dit.py:489-498.
+ * q: view of q->len query tokens; k, v: views of the same number of key tokens
+ *   (k->len > 0), all [len, num_heads, head_dim] with 16-byte aligned rows.
+ * out: caller-allocated bf16 [q->len, num_heads, head_dim], heads dense, token stride
+ *   out_stride_token (elements, >= num_heads * head_dim), 16-byte aligned rows.
+ * head_dim must be 128 (JOY_ERR_UNSUPPORTED otherwise). scale > 0 (1/sqrt(head_dim)
+ * reproduces the reference default).
+ */
+JOY_API joy_status joy_attention_fwd(const joy_bf16_view *q, const joy_bf16_view *k, const joy_bf16_view *v,
+                                     void *out, int64_t out_stride_token, int64_t num_heads, int64_t head_dim,
+                                     float scale, void *stream);
 
 /*
  * (Layer|RMS)Norm + adaLN scale/shift.

@@ -1,5 +1,6 @@
 // C ABI of libjoyomni_hip: argument validation (mirroring the reference's
 // TORCH_CHECKs), then one kernel launch on the caller's stream.
+#include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -463,6 +464,43 @@ joy_status joy_fused_cached_kv_pack(const joy_bf16_view* key0, const joy_bf16_vi
   a.len1 = len1;
   a.heads = (int)num_heads;
   return hip_status(joy::launch_cached_kv_pack(a, (hipStream_t)stream), "fused_cached_kv_pack launch");
+}
+
+
+joy_status joy_attention_fwd(const joy_bf16_view* q, const joy_bf16_view* k, const joy_bf16_view* v, void* out,
+                             int64_t out_stride_token, int64_t num_heads, int64_t head_dim, float scale,
+                             void* stream) {
+  if (head_dim != 128) return fail(JOY_ERR_UNSUPPORTED, "attention_fwd supports head_dim=128 only");
+  if (!q || !k || !v) return fail(JOY_ERR_INVALID_ARGUMENT, "q, k and v views must be non-null");
+  if (q->len < 0 || k->len < 0 || v->len != k->len)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "key and value must have the same sequence length");
+  if (num_heads <= 0 || num_heads > 65535) return fail(JOY_ERR_INVALID_ARGUMENT, "num_heads must be in [1, 65535]");
+  if (!(scale > 0.0f) || !(scale < INFINITY)) return fail(JOY_ERR_INVALID_ARGUMENT, "scale must be positive and finite");
+  if (out_stride_token < num_heads * head_dim)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "out token stride must be >= num_heads * head_dim");
+  if (q->len == 0) return ok();
+  if (k->len == 0) return fail(JOY_ERR_INVALID_ARGUMENT, "attention over an empty key sequence is undefined");
+  if (!present(q) || !present(k) || !present(v) || !out)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "q, k, v and out must be non-null");
+  const joy_bf16_view* views[3] = {q, k, v};
+  for (const joy_bf16_view* w : views) {
+    if (!aligned(w->ptr, 16) || w->stride_token % 8 != 0 || w->stride_head % 8 != 0)
+      return fail(JOY_ERR_UNSUPPORTED, "q, k, v need 16-byte aligned rows (pointer and strides multiples of 8)");
+  }
+  if (!aligned(out, 16) || out_stride_token % 8 != 0)
+    return fail(JOY_ERR_UNSUPPORTED, "out needs 16-byte aligned rows");
+  if ((q->len + 127) / 128 > 0x7fffffffLL) return fail(JOY_ERR_UNSUPPORTED, "sequence too long");
+  joy::AttnArgs a;
+  a.q = row_view(q);
+  a.k = row_view(k);
+  a.v = row_view(v);
+  a.out = (uint16_t*)out;
+  a.out_stride_token = out_stride_token;
+  a.q_len = q->len;
+  a.k_len = k->len;
+  a.heads = (int)num_heads;
+  a.scale_log2e = scale * 1.4426950408889634f;
+  return hip_status(joy::launch_attention_fwd(a, (hipStream_t)stream), "attention_fwd launch");
 }
 
 }  // extern "C"

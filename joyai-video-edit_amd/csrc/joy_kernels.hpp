@@ -85,6 +85,16 @@ struct CachedPackArgs {
   int heads;
 };
 
+// Attention forward: bf16 [len, H, 128] views; out [q_len, H, 128] with token stride.
+struct AttnArgs {
+  RowView q, k, v;
+  uint16_t* out;
+  int64_t out_stride_token;
+  int64_t q_len, k_len;
+  int heads;
+  float scale_log2e;  // softmax scale * log2(e)
+};
+
 // (Layer|RMS)Norm + adaLN scale/shift, optionally + per-token FP8 of the output.
 struct NormModArgs {
   const void* x;        // [M, N] rows with stride x_stride (elements)
@@ -113,5 +123,6 @@ int64_t fp8_gemm_workspace_bytes(int M, int N, int K);
 hipError_t launch_norm_modulate(const NormModArgs& a, hipStream_t st);
 hipError_t launch_joint_qkv_pack(const JointPackArgs& a, hipStream_t st);
 hipError_t launch_cached_kv_pack(const CachedPackArgs& a, hipStream_t st);
+hipError_t launch_attention_fwd(const AttnArgs& a, hipStream_t st);
 
 }  // namespace joy

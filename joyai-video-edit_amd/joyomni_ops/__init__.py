@@ -20,6 +20,7 @@ torch device composition, so the reference's imports
 from __future__ import annotations
 
 import ctypes
+import math
 from typing import Optional
 
 import torch
@@ -46,6 +47,8 @@ __all__ = [
     "fp8_scaled_mm_gated_residual",
     "fused_cached_kv_pack_out",
     "fused_text_qkv_pack",
+    "sdpa_attention",
+    "sdpa_attention_out",
 ]
 
 _NS = "joyomni_ops"
@@ -97,6 +100,10 @@ _lib_def.define(
 _lib_def.define(
     "fused_text_qkv_pack(Tensor txt_q, Tensor txt_k, Tensor txt_v, Tensor txt_q_weight, "
     "Tensor txt_k_weight, float eps, Tensor(a!) out_q, Tensor(b!) out_k, Tensor(c!) out_v) -> ()")
+
+_lib_def.define("sdpa_attention(Tensor query, Tensor key, Tensor value, float? scale=None) -> Tensor")
+_lib_def.define(
+    "sdpa_attention_out(Tensor query, Tensor key, Tensor value, Tensor(a!) out, float? scale=None) -> ()")
 
 _ops = torch.ops.joyomni_ops
 
@@ -378,6 +385,47 @@ def _view(t: Optional[torch.Tensor]):
 
 def _vref(v):
     return None if v is None else ctypes.byref(v)
+
+
+# --------------------------------------------------------------------------
+# attention core
+# --------------------------------------------------------------------------
+def _attention_checks(query, key, value, out):
+    for name, t in (("query", query), ("key", key), ("value", value), ("out", out)):
+        _check(t.is_cuda, f"{name} must be a CUDA tensor")
+        _check(t.dim() == 4, f"{name} must be [B, S, H, D]")
+        _check(t.dtype == torch.bfloat16, f"{name} must be bfloat16")
+        _check(t.stride(3) == 1 or t.size(3) <= 1, f"{name} last dimension must be contiguous")
+    B, Lq, H, D = query.shape
+    _check(key.shape == value.shape, "key and value must have the same shape")
+    _check(key.size(0) == B and key.size(2) == H and key.size(3) == D,
+           "query, key and value must agree in batch, heads and head_dim")
+    _check(tuple(out.shape) == (B, Lq, H, D), "out must have the shape of query")
+    _check(out.stride(2) == D, "out heads must be dense (stride(2) == head_dim)")
+    return B, Lq, H, D
+
+
+def _attention_impl(query, key, value, out, scale):
+    B, Lq, H, D = _attention_checks(query, key, value, out)
+    sc = float(scale) if scale is not None else 1.0 / math.sqrt(D)
+    with torch.cuda.device(query.device):
+        for b in range(B):
+            qv, kv, vv = _view(query[b:b + 1]), _view(key[b:b + 1]), _view(value[b:b + 1])
+            st = _LIB.joy_attention_fwd(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv),
+                                        out[b].data_ptr(), out.stride(1), H, D, sc, _stream(query))
+            _lib.check(_LIB, st)
+
+
+@torch.library.impl(_lib_def, "sdpa_attention", "CUDA")
+def _sdpa_attention_cuda(query, key, value, scale=None):
+    out = torch.empty(query.shape, device=query.device, dtype=query.dtype)
+    _attention_impl(query, key, value, out, scale)
+    return out
+
+
+@torch.library.impl(_lib_def, "sdpa_attention_out", "CUDA")
+def _sdpa_attention_out_cuda(query, key, value, out, scale=None):
+    _attention_impl(query, key, value, out, scale)
 
 
 @torch.library.impl(_lib_def, "fused_joint_qkv_pack", "CUDA")
@@ -669,6 +717,16 @@ def _fake_fused_cached_kv_pack_out(key0, value0, key1, value1, cos, sin, out_k, 
     return None
 
 
+@torch.library.register_fake("joyomni_ops::sdpa_attention")
+def _fake_sdpa_attention(query, key, value, scale=None):
+    return query.new_empty(query.shape)
+
+
+@torch.library.register_fake("joyomni_ops::sdpa_attention_out")
+def _fake_sdpa_attention_out(query, key, value, out, scale=None):
+    return None
+
+
 @torch.library.register_fake("joyomni_ops::fused_text_qkv_pack")
 def _fake_fused_text_qkv_pack(txt_q, txt_k, txt_v, txt_q_weight, txt_k_weight, eps, out_q, out_k, out_v):
     return None
@@ -775,3 +833,16 @@ def fused_text_qkv_pack(txt_q, txt_k, txt_v, txt_q_weight, txt_k_weight, eps, ou
     """The condition segment of fused_joint_qkv_pack (two-rounding q/k RMSNorm, V copied) written
     into caller-provided dense [1, T, H, D] outputs (the tails of the joint Q / K / V)."""
     _ops.fused_text_qkv_pack(txt_q, txt_k, txt_v, txt_q_weight, txt_k_weight, eps, out_q, out_k, out_v)
+
+
+def sdpa_attention(query, key, value, scale: Optional[float] = None):
+    """softmax(q k^T * scale) v per head on [B, S, H, D] bf16 tensors, non-causal, no mask:
+    the reference's ``_sdpa_attention`` (dit.py:154-167) without its transposes. scale defaults
+    to 1/sqrt(D) like F.scaled_dot_product_attention; head_dim 128."""
+    return _ops.sdpa_attention(query, key, value, scale)
+
+
+def sdpa_attention_out(query, key, value, out, scale: Optional[float] = None):
+    """sdpa_attention writing into ``out`` ([B, S, H, D], dense heads), e.g. rows of a
+    [S, H*D] buffer that the out-projection quantiser reads."""
+    _ops.sdpa_attention_out(query, key, value, out, scale)

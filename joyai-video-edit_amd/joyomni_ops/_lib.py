@@ -64,6 +64,7 @@ SIGNATURES = {
         _int, [_view, _view, _view, _vp, _vp, _f32, _i64, _i64, _vp, _vp, _vp, _vp]),
     "joy_fused_cached_kv_pack": (
         _int, [_view, _view, _view, _view, _vp, _vp, _i64, _i64, _vp, _vp, _vp]),
+    "joy_attention_fwd": (_int, [_view, _view, _view, _vp, _i64, _i64, _i64, _f32, _vp]),
     "joy_fused_norm_scale_shift": (
         _int, [_vp, _i64, _int, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _int, _f32, _vp]),
     "joy_fused_norm_scale_shift_fp8": (
@@ -71,7 +72,7 @@ SIGNATURES = {
                _vp]),
 }
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 
 class JoyError(RuntimeError):

@@ -17,6 +17,8 @@ paths this repository implements on MI355X:
 * ``oracle.kvpack``  -- joint-attention Q/K/V pack with the two-rounding text
   RMSNorm and the rotation of pre-RoPE cached K
   (``joyomni_ops/csrc/fused_joint_qkv_pack.cu:58-220``).
+* ``oracle.attention`` -- the joint-attention core, softmax(q k^T / sqrt(D)) v
+  (``deploy/xvideo/models/dit/dit.py:154-167``).
 * ``oracle.rope``    -- 3-D (t,h,w) RoPE tables (``deploy/xvideo/models/dit/rope.py:31-52``,
   ``dit.py:896-934``, ``sgl_fused_ops.py:94-119``).
 * ``oracle.torch_path`` -- the reference's own CPU torch code path, restated,

@@ -1,0 +1,139 @@
+"""GPU parity: joint-attention core (joyomni_ops.sdpa_attention, joy_attention_fwd) vs the
+float64 oracle (oracle/attention.py, restating dit.py:154-167).
+
+Tolerance (bf16 output, probabilities rounded to bf16 for the P V product as in bf16
+flash attention): |out - ref| <= 2^-8 * (max_j |v[j, h, :]| + |ref|) per element. Exact
+cases (single key, identical keys over small-integer values) are checked bit for bit."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import DEV, announce, gen, u16
+from oracle import attention as oa
+from oracle.fp8 import bf16_to_f32, f32_to_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(Lq, Lk, H, seed, scale=1.0):
+    g = gen(seed)
+    q = (torch.randn(Lq, H, 128, generator=g) * scale).to(torch.bfloat16)
+    k = (torch.randn(Lk, H, 128, generator=g) * scale).to(torch.bfloat16)
+    v = torch.randn(Lk, H, 128, generator=g).to(torch.bfloat16)
+    return q, k, v
+
+
+def _run(q, k, v, scale=None):
+    import joyomni_ops as jo
+    out = jo.sdpa_attention(q[None].to(DEV), k[None].to(DEV), v[None].to(DEV), scale)
+    torch.cuda.synchronize()
+    return out[0]
+
+
+def _check(out, q, k, v, what, scale=None, rows=None):
+    ref = oa.sdpa(u16(q if rows is None else q[rows]), u16(k), u16(v), scale)
+    got = bf16_to_f32(u16(out if rows is None else out[torch.from_numpy(rows).to(out.device)]))
+    vmax = np.abs(bf16_to_f32(u16(v))).max(axis=0)  # [H, D] -> per head max below
+    tol = 2.0 ** -8 * (vmax.max(axis=-1)[None, :, None] + np.abs(ref))
+    err = np.abs(got - ref)
+    assert (err <= tol).all(), f"{what}: {np.count_nonzero(err > tol)} elements beyond tolerance, max err {err.max():.3e}"
+    return err.max()
+
+
+@pytest.mark.parametrize("Lq,Lk,H", [(1, 1, 1), (5, 3, 2), (128, 64, 1), (130, 65, 2), (300, 700, 3),
+                                     (257, 129, 4), (64, 1000, 1)])
+def test_random_shapes(Lq, Lk, H):
+    announce("attention random", Lq, Lk, H)
+    q, k, v = _inputs(Lq, Lk, H, Lq * 31 + Lk)
+    _check(_run(q, k, v), q, k, v, f"{Lq}x{Lk}x{H}")
+
+
+def test_peaked_scores_and_explicit_scale():
+    """Large-magnitude q/k (peaked softmax, exp2 range) and a non-default scale."""
+    announce("attention peaked")
+    q, k, v = _inputs(200, 333, 2, 7, scale=3.0)
+    _check(_run(q, k, v), q, k, v, "peaked")
+    _check(_run(q, k, v, 0.02), q, k, v, "scale 0.02", scale=0.02)
+
+
+def test_single_key_is_exact():
+    announce("attention single key")
+    q, k, v = _inputs(77, 1, 3, 11)
+    assert np.array_equal(u16(_run(q, k, v)), np.broadcast_to(u16(v), (77, 3, 128)))
+
+
+def test_identical_keys_exact_mean():
+    """64 identical keys: every probability is exactly 1, small-integer values sum exactly,
+    so the output is the bf16 rounding of their mean."""
+    announce("attention identical keys")
+    rng = np.random.default_rng(5)
+    H = 2
+    q = torch.from_numpy(rng.standard_normal((40, H, 128)).astype(np.float32)).to(torch.bfloat16)
+    k = torch.from_numpy(np.repeat(rng.standard_normal((1, H, 128)).astype(np.float32), 64, axis=0)
+                         ).to(torch.bfloat16)
+    v = torch.from_numpy(rng.integers(-8, 9, (64, H, 128)).astype(np.float32)).to(torch.bfloat16)
+    exp = f32_to_bf16((bf16_to_f32(u16(v)).astype(np.float64).mean(axis=0)).astype(np.float32))
+    assert np.array_equal(u16(_run(q, k, v)), np.broadcast_to(exp, (40, H, 128)))
+
+
+def test_strided_views_and_out_rows():
+    """q/k/v read as head/token-strided slices of fused [L, 3, H, D] rows; output written into
+    the rows of a wider [L, H*D + 64] buffer (only the [:, :H*D] part may change)."""
+    announce("attention strided")
+    import joyomni_ops as jo
+    L, H = 190, 2
+    g = gen(3)
+    qkv = torch.randn(L, 3, H, 128, generator=g).to(torch.bfloat16).to(DEV)
+    q, k, v = qkv[None, :, 0], qkv[None, :, 1], qkv[None, :, 2]
+    buf = torch.full((L, H * 128 + 64), 7.0, dtype=torch.bfloat16, device=DEV)
+    out = buf[:, :H * 128].view(1, L, H, 128)
+    jo.sdpa_attention_out(q, k, v, out)
+    torch.cuda.synchronize()
+    assert bool((buf[:, H * 128:] == 7.0).all())
+    _check(out[0], q[0].cpu(), k[0].cpu(), v[0].cpu(), "strided")
+
+
+def test_batch_of_two():
+    announce("attention batch 2")
+    import joyomni_ops as jo
+    g = gen(4)
+    q = torch.randn(2, 70, 2, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(2, 90, 2, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(2, 90, 2, 128, generator=g).to(torch.bfloat16)
+    out = jo.sdpa_attention(q.to(DEV), k.to(DEV), v.to(DEV))
+    torch.cuda.synchronize()
+    for b in range(2):
+        _check(out[b], q[b], k[b], v[b], f"batch {b}")
+
+
+def test_argument_errors():
+    import joyomni_ops as jo
+    q = torch.zeros(1, 4, 2, 64, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError, match="head_dim=128"):
+        jo.sdpa_attention(q, q, q)
+    q = torch.zeros(1, 4, 2, 128, dtype=torch.bfloat16, device=DEV)
+    k = torch.zeros(1, 0, 2, 128, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError, match="empty key"):
+        jo.sdpa_attention(q, k, k)
+
+
+def test_cfg4_joint_shape_sampled_queries():
+    """The block's joint attention: 10800 + 512 queries over 2 x 10800 cached + 10800 + 512 keys,
+    40 heads. 64 sampled queries (queries are independent) against the oracle; torch's SDPA
+    (the reference's own call) on the same inputs is held to the same tolerance."""
+    announce("attention cfg4 11312 x 32912 x 40")
+    Lq, Lk, H = 11312, 32912, 40
+    q, k, v = _inputs(Lq, Lk, H, 2024)
+    qd, kd, vd = q[None].to(DEV), k[None].to(DEV), v[None].to(DEV)
+    import joyomni_ops as jo
+    out = jo.sdpa_attention(qd, kd, vd)[0]
+    ref_sdpa = torch.nn.functional.scaled_dot_product_attention(
+        qd.transpose(1, 2), kd.transpose(1, 2), vd.transpose(1, 2), is_causal=False).transpose(1, 2)[0]
+    torch.cuda.synchronize()
+    rows = np.sort(np.random.default_rng(9).choice(Lq, 64, replace=False))
+    rows[-1] = Lq - 1
+    err_ours = _check(out, q, k, v, "cfg4 ours", rows=rows)
+    err_sdpa = _check(ref_sdpa, q, k, v, "cfg4 torch sdpa", rows=rows)
+    print(f"cfg4 max|err| vs float64: ours {err_ours:.3e}, torch SDPA {err_sdpa:.3e}")
