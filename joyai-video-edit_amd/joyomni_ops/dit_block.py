@@ -23,8 +23,9 @@ per stream (video "img", condition "txt"), with ``mod = table + vec`` split into
     (``fused_cached_kv_pack_out``, ``_concat_kv_entries`` ``dit.py:216-271``);
   - condition stream: the two-rounding q/k RMSNorm into the tails
     (``fused_text_qkv_pack``);
-* attention: PyTorch SDPA, non-causal, no mask (``dit.py:154-167``), restricted to
-  its fused flash / memory-efficient kernels;
+* attention: the gfx950 flash-attention kernel (``sdpa_attention``), non-causal, no
+  mask, default scale 1/sqrt(D) -- the reference's ``_sdpa_attention``
+  (``dit.py:154-167``) read in the token-major joint layout without transposes;
 * out-proj FP8 GEMM with the gated residual (``fused_add_gate``, ``dit.py:525-528``)
   in its epilogue (``fp8_scaled_mm_gated_residual``);
 * adaLN + FP8 quant -> FFN-up FP8 GEMM with the GELU-tanh epilogue -> quant ->
@@ -44,10 +45,9 @@ from typing import Callable, List, Optional, Sequence, Tuple
 
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 
 from . import (fused_cached_kv_pack_out, fused_norm_scale_shift_fp8, fused_qkv_norm_rope_cache,
-               fused_text_qkv_pack)
+               fused_text_qkv_pack, sdpa_attention)
 from .fp8_linear import Fp8Linear, exact_division_for
 
 NORM_EPS = 1e-6            # dit.py:35
@@ -148,12 +148,8 @@ class QuantizedDoubleStreamBlock:
 
     @staticmethod
     def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
-        """SDPA on [B, S, H, D] operands (dit.py:154-167), fused kernels only."""
-        from torch.nn.attention import SDPBackend, sdpa_kernel
-        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
-            out = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
-                                                 is_causal=False)
-        return out.transpose(1, 2)
+        """Attention on [B, S, H, D] operands (dit.py:154-167): [B, S, H, D] out, heads dense."""
+        return sdpa_attention(q, k, v)
 
     # -- forward ------------------------------------------------------------
     def forward(self, img: torch.Tensor, txt: torch.Tensor, vec: torch.Tensor, img_cos: torch.Tensor,
