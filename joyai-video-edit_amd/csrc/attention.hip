@@ -22,12 +22,15 @@
 //     ds_read_b64_tr_b16 per MFMA, whose addresses apply the same permutation. The
 //     O^T accumulator again gives each lane one query, so the rescale by
 //     exp2(m_old - m_new) is per lane.
-// K and V tiles travel global -> VGPR -> LDS (double-buffered, one barrier per
-// tile); LDS rows of 256 bytes store 16-byte chunk c at c ^ (row & 15).
+// K and V tiles reach LDS by direct-to-LDS DMA (double-buffered, the next tile in flight
+// during the current one, one barrier per tile); LDS rows of 256 bytes store 16-byte
+// chunk c at c ^ (row & 15).
 //
 // ds_read_b64_tr_b16 lane layout (measured on gfx950): within each group of 16
 // lanes, lane a points at 4 consecutive 16-bit values M[a][0..3] and lane i receives
 // M[4j + i/4][i % 4] for j = 0..3.
+#include <type_traits>
+
 #include "joy_common.hpp"
 #include "joy_kernels.hpp"
 
@@ -37,12 +40,15 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kD = 128;
-constexpr int kBQ = 128;               // queries per workgroup
 constexpr int kBK = 64;                // keys per tile
 constexpr int kRowB = kD * 2;          // bytes per K / V row
 constexpr int kTileB = kBK * kRowB;    // 16 KB per K or V tile
+
+template <int J>
+using IC = std::integral_constant<int, J>;
 
 __device__ __forceinline__ int chunk_at(int row, int chunk) { return row * kRowB + ((chunk ^ (row & 15)) << 4); }
 
@@ -52,44 +58,82 @@ __device__ __forceinline__ v16f mfma_bf16(const bf16x8& a, const bf16x8& b, cons
 
 __device__ __forceinline__ bf16x8 as_bf16x8(const v4i& v) { return __builtin_bit_cast(bf16x8, v); }
 
-__global__ __launch_bounds__(256, 2) void attn_fwd_d128(AttnArgs a) {
+// Combine a value with the one of lane ^ 32 without the LDS crossbar: v_permlane32_swap
+// with both operands x returns {x[lane], x[lane ^ 32]} (in an order that depends on the
+// half, measured on gfx950), and both halves add them in the same order.
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// QB query blocks of 32 per wave (workgroup = 4 waves x 32 QB queries): with QB = 2 every K
+// fragment and every V^T operand read from LDS feeds two MFMAs.
+template <int QB>
+__global__ __launch_bounds__(256, QB == 1 ? 2 : 1) void attn_fwd_d128(AttnArgs a) {
+  constexpr int BQ = 4 * 32 * QB;
   __shared__ __attribute__((aligned(16))) uint8_t lds[2][2][kTileB];  // [buffer][K, V]
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int head = blockIdx.y;
   const int ql = lane & 31, hf = lane >> 5;
-  const int q = blockIdx.x * kBQ + wave * 32 + ql;  // this lane's query
   const int64_t Lq = a.q_len, Lk = a.k_len;
+  int qrow[QB];
+#pragma unroll
+  for (int i = 0; i < QB; ++i) qrow[i] = blockIdx.x * BQ + (wave * QB + i) * 32 + ql;  // this lane's queries
 
   // Q as the B operand of S^T = K Q^T: lane holds Q[q][16 s + 8 hf .. +8], s = 0..7
-  v4i qf[8];
-  {
-    const uint16_t* qp = a.q.ptr + (int64_t)min((int64_t)q, Lq - 1) * a.q.stride_token +
+  v4i qf[QB][8];
+#pragma unroll
+  for (int i = 0; i < QB; ++i) {
+    const uint16_t* qp = a.q.ptr + (int64_t)min((int64_t)qrow[i], Lq - 1) * a.q.stride_token +
                          (int64_t)head * a.q.stride_head + 8 * hf;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) qf[s] = *(const v4i*)(qp + 16 * s);
+    for (int st = 0; st < 8; ++st) qf[i][st] = *(const v4i*)(qp + 16 * st);
   }
 
-  // K / V tile loads: thread chunk c = tid + 256 i covers row c / 16, 16-byte chunk c % 16
+  // K / V tiles reach LDS by direct-to-LDS DMA: one 16-byte load per lane and instruction
+  // writes 1 KB = 4 LDS rows; lane l lands in row 4 i + l / 16, physical chunk l % 16, so it
+  // fetches logical chunk (l % 16) ^ (row & 15) of that key row. Each wave moves 4 KB of K
+  // and 4 KB of V per tile (16 rows each).
+  // lane source pointers of the wave's 4 K and 4 V rows in the current tile, advanced by one
+  // tile per iteration; the partial last tile recomputes them with the key clamped to Lk - 1
   const uint16_t* kbase = a.k.ptr + (int64_t)head * a.k.stride_head;
   const uint16_t* vbase = a.v.ptr + (int64_t)head * a.v.stride_head;
-  v4i ks[4], vs[4];
-  auto gload = [&](int64_t k0) {
+  const uint16_t* kp[4];
+  const uint16_t* vp[4];
+  auto set_ptrs = [&](int64_t k0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int c = tid + 256 * i;
-      const int64_t key = min(k0 + (c >> 4), Lk - 1);
-      ks[i] = *(const v4i*)(kbase + key * a.k.stride_token + (c & 15) * 8);
-      vs[i] = *(const v4i*)(vbase + key * a.v.stride_token + (c & 15) * 8);
+      const int row = wave * 16 + i * 4 + (lane >> 4);
+      const int64_t key = min(k0 + row, Lk - 1);
+      const int chunk = (lane & 15) ^ (row & 15);
+      kp[i] = kbase + key * a.k.stride_token + chunk * 8;
+      vp[i] = vbase + key * a.v.stride_token + chunk * 8;
     }
   };
-  auto lwrite = [&](int buf) {
+  auto dma_tile = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int c = tid + 256 * i;
-      const int off = chunk_at(c >> 4, c & 15);
-      *(v4i*)(&lds[buf][0][off]) = ks[i];
-      *(v4i*)(&lds[buf][1][off]) = vs[i];
+      __builtin_amdgcn_global_load_lds((const void*)kp[i], (lds_void*)(&lds[buf][0][(wave * 16 + i * 4) * kRowB]),
+                                       16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)vp[i], (lds_void*)(&lds[buf][1][(wave * 16 + i * 4) * kRowB]),
+                                       16, 0, 0);
+    }
+  };
+  const int64_t k_step = (int64_t)kBK * a.k.stride_token, v_step = (int64_t)kBK * a.v.stride_token;
+  auto next_tile = [&](int64_t k0) {  // pointers of the tile starting at key k0 (= previous + kBK)
+    if (k0 + kBK <= Lk) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        kp[i] += k_step;
+        vp[i] += v_step;
+      }
+    } else {
+      set_ptrs(k0);
     }
   };
 
@@ -99,79 +143,105 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_d128(AttnArgs a) {
   const int tr_row = 4 * hf + (ta >> 2);
   const int tr_col = 16 * (tg & 1) + 4 * (ta & 3);  // element column within a 32-wide d block
 
-  v16f o[4];
+  v16f o[QB][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) o[i] = (v16f){};
-  float m_run = -INFINITY, l_run = 0.f;
+  for (int i = 0; i < QB; ++i)
+#pragma unroll
+    for (int db = 0; db < 4; ++db) o[i][db] = (v16f){};
+  float m_run[QB], l_run[QB];
+#pragma unroll
+  for (int i = 0; i < QB; ++i) m_run[i] = -INFINITY, l_run[i] = 0.f;
   const float sl2 = a.scale_log2e;
 
   const int64_t ntiles = (Lk + kBK - 1) / kBK;
-  gload(0);
-  lwrite(0);
-  if (ntiles > 1) gload(kBK);
-  for (int64_t t = 0; t < ntiles; ++t) {
-    const int buf = (int)(t & 1);
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): own LDS writes done
+  set_ptrs(0);
+  dma_tile(0);
+  // one tile; the buffer index is a template constant (the loop runs two tiles per trip), so
+  // every LDS address is a loop-invariant lane offset plus an immediate
+  auto tile = [&](auto bufc, int64_t t) {
+    constexpr int buf = decltype(bufc)::value;
+    // own DMAs of tile t landed (nothing else is outstanding); after the barrier every wave's
+    // have, and every wave has finished tile t-1, whose buffer the next DMA overwrites
+    __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0), lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
+    if (t + 1 < ntiles) {
+      next_tile((t + 1) * kBK);
+      dma_tile(buf ^ 1);
+    }
     const uint8_t* kt = lds[buf][0];
     const uint8_t* vt = lds[buf][1];
 
-    // S^T for two 32-key blocks
-    v16f s[2];
+    // raw scores S^T for two 32-key blocks; each K fragment feeds the QB query blocks
+    // (the MFMA blocks run at raised wave priority, so that of the two waves on a SIMD the
+    // one with MFMAs to issue gets the pipe while the other works through its softmax)
+    __builtin_amdgcn_s_setprio(1);
+    v16f s[QB][2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      s[kb] = (v16f){};
+#pragma unroll
+      for (int i = 0; i < QB; ++i) s[i][kb] = (v16f){};
       const int row = kb * 32 + ql;
 #pragma unroll
       for (int st = 0; st < 8; ++st) {
         const v4i kf = *(const v4i*)(kt + chunk_at(row, 2 * st + hf));
-        s[kb] = mfma_bf16(as_bf16x8(kf), as_bf16x8(qf[st]), s[kb]);
+#pragma unroll
+        for (int i = 0; i < QB; ++i) s[i][kb] = mfma_bf16(as_bf16x8(kf), as_bf16x8(qf[i][st]), s[i][kb]);
       }
     }
-    // online softmax; keys past Lk (only in the last tile) get -inf
+
+    __builtin_amdgcn_s_setprio(0);
+    // online softmax in log2 units (scale folded into one fma); keys past Lk get -inf
     const int64_t k0 = t * kBK;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) s[kb] *= sl2;
     if (k0 + kBK > Lk) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int64_t key = k0 + kb * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
-          if (key >= Lk) s[kb][r] = -INFINITY;
+          if (key >= Lk)
+#pragma unroll
+            for (int i = 0; i < QB; ++i) s[i][kb][r] = -INFINITY;
         }
     }
-    float mt = -INFINITY;
+    v4i pb[QB][4];  // P^T B operands, 16 keys each: chunk 2 kb + b = registers 8 b .. 8 b + 7 of s[kb]
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int i = 0; i < QB; ++i) {
+      float mt = -INFINITY;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[kb][r]);
-    mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
-    const float m_new = fmaxf(m_run, mt);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-    float rs = 0.f;
-    v4i pb[4];  // P^T B operands, 16 keys each: chunk 2 kb + b = registers 8 b .. 8 b + 7 of s[kb]
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+        for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[i][kb][r]);
+      mt = xor32_max(mt);
+      const float m_new = fmaxf(m_run[i], mt * sl2);
+      const float alpha = __builtin_amdgcn_exp2f(m_run[i] - m_new);
+      float rs = 0.f;
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        float p[8];
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          p[j] = __builtin_amdgcn_exp2f(s[kb][8 * b + j] - m_new);
-          rs += p[j];
+        for (int b = 0; b < 2; ++b) {
+          float p[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            p[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i][kb][8 * b + j], sl2, -m_new));
+            rs += p[j];
+          }
+          pb[i][2 * kb + b] = (v4i){(int)pack_bf16x2(p[0], p[1]), (int)pack_bf16x2(p[2], p[3]),
+                                    (int)pack_bf16x2(p[4], p[5]), (int)pack_bf16x2(p[6], p[7])};
         }
-        pb[2 * kb + b] = (v4i){(int)pack_bf16x2(p[0], p[1]), (int)pack_bf16x2(p[2], p[3]),
-                               (int)pack_bf16x2(p[4], p[5]), (int)pack_bf16x2(p[6], p[7])};
-      }
-    rs += __shfl_xor(rs, 32, kWave);
-    l_run = l_run * alpha + rs;
-    m_run = m_new;
+      rs = xor32_sum(rs);
+      l_run[i] = l_run[i] * alpha + rs;
+      m_run[i] = m_new;
+      // rescale only when some lane's running max moved (alpha == 1 otherwise)
+      if (__builtin_amdgcn_read_exec() &&
+          __builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] *= alpha;
+        for (int db = 0; db < 4; ++db) o[i][db] *= alpha;
+      }
+    }
 
-    // O^T += V^T P^T
+    // O^T += V^T P^T; each V^T operand feeds the QB query blocks
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -186,29 +256,35 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_d128(AttnArgs a) {
           const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
               (lds_s16x4*)(vt + chunk_at(row0 + 8, chunk) + within));
           const v4i va = __builtin_bit_cast(v4i, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-          o[db] = mfma_bf16(as_bf16x8(va), as_bf16x8(pb[2 * kb + b]), o[db]);
+#pragma unroll
+          for (int i = 0; i < QB; ++i) o[i][db] = mfma_bf16(as_bf16x8(va), as_bf16x8(pb[i][2 * kb + b]), o[i][db]);
         }
       }
+    __builtin_amdgcn_s_setprio(0);
 
-    // tile t+1 (in registers) into the other buffer; then start loading tile t+2
-    if (t + 1 < ntiles) {
-      lwrite(buf ^ 1);
-      if (t + 2 < ntiles) gload((t + 2) * kBK);
-    }
+  };
+  int64_t t = 0;
+  for (; t + 2 <= ntiles; t += 2) {
+    tile(IC<0>{}, t);
+    tile(IC<1>{}, t + 1);
   }
+  if (t < ntiles) tile(IC<0>{}, t);
+  __builtin_amdgcn_s_waitcnt(0x0070);  // (no DMA outstanding past the loop)
 
   // O = O^T / l: lane holds query q, d = 32 db + 8 (r / 4) + 4 hf + (r % 4)
-  if (q < Lq) {
-    const float inv = 1.0f / l_run;
-    uint16_t* op = a.out + (int64_t)q * a.out_stride_token + (int64_t)head * kD;
+#pragma unroll
+  for (int i = 0; i < QB; ++i) {
+    if (qrow[i] >= Lq) continue;
+    const float inv = 1.0f / l_run[i];
+    uint16_t* op = a.out + (int64_t)qrow[i] * a.out_stride_token + (int64_t)head * kD;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
         const int d = db * 32 + 8 * r4 + 4 * hf;
         uint2 w;
-        w.x = pack_bf16x2(o[db][4 * r4] * inv, o[db][4 * r4 + 1] * inv);
-        w.y = pack_bf16x2(o[db][4 * r4 + 2] * inv, o[db][4 * r4 + 3] * inv);
+        w.x = pack_bf16x2(o[i][db][4 * r4] * inv, o[i][db][4 * r4 + 1] * inv);
+        w.y = pack_bf16x2(o[i][db][4 * r4 + 2] * inv, o[i][db][4 * r4 + 3] * inv);
         *(uint2*)(op + d) = w;
       }
   }
@@ -216,9 +292,14 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_d128(AttnArgs a) {
 
 }  // namespace
 
+// One query block per wave: with two, every K / V^T operand read feeds two MFMAs, but the
+// registers spill and one workgroup fills a CU; measured at the cfg-4 joint shape (11312 x
+// 32912 x 40 heads): 8.8 ms with QB = 1 against 15.3 ms with QB = 2.
 hipError_t launch_attention_fwd(const AttnArgs& a, hipStream_t st) {
-  const dim3 grid((unsigned)((a.q_len + kBQ - 1) / kBQ), (unsigned)a.heads);
-  hipLaunchKernelGGL(attn_fwd_d128, grid, dim3(256), 0, st, a);
+  constexpr int QB = 1;
+  constexpr int BQ = 4 * 32 * QB;
+  const dim3 grid((unsigned)((a.q_len + BQ - 1) / BQ), (unsigned)a.heads);
+  hipLaunchKernelGGL(attn_fwd_d128<QB>, grid, dim3(256), 0, st, a);
   return hipGetLastError();
 }
 
