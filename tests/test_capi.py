@@ -197,3 +197,23 @@ def test_norm_argument_checks(lib):
             "bfloat16 or float16")
     _status(lib, g(p, 64, 0, None, None, p, p, 1, None, p, p, 7, 4, 64, 0, 1e-6, None), 1, "rounding")
     _status(lib, g(p, 64, 0, None, None, p, p, 1, None, None, p, 0, 4, 64, 0, 1e-6, None), 1, "output_q")
+
+
+def test_attention_argument_checks(lib):
+    V = _lib.Bf16View
+    good = V(0x1000, 8, 256, 128)
+    keys = V(0x2000, 16, 256, 128)
+    f = lib.joy_attention_fwd
+    b = ctypes.byref
+    out = ctypes.c_void_p(0x4000)
+    _status(lib, f(b(good), b(keys), b(keys), out, 256, 2, 64, 0.1, None), 2, "head_dim=128")
+    _status(lib, f(None, b(keys), b(keys), out, 256, 2, 128, 0.1, None), 1, "views must be non-null")
+    _status(lib, f(b(good), b(keys), b(V(0x3000, 15, 256, 128)), out, 256, 2, 128, 0.1, None), 1,
+            "same sequence length")
+    _status(lib, f(b(good), b(V(0, 0, 256, 128)), b(V(0, 0, 256, 128)), out, 256, 2, 128, 0.1, None), 1,
+            "empty key sequence")
+    _status(lib, f(b(good), b(keys), b(keys), out, 128, 2, 128, 0.1, None), 1, "out token stride")
+    _status(lib, f(b(good), b(keys), b(keys), out, 256, 2, 128, -1.0, None), 1, "scale must be positive")
+    _status(lib, f(b(V(0x1008, 8, 256, 128)), b(keys), b(keys), out, 256, 2, 128, 0.1, None), 2,
+            "16-byte aligned rows")
+    assert f(b(V(0, 0, 256, 128)), b(keys), b(keys), out, 256, 2, 128, 0.1, None) == 0  # no queries: no launch
