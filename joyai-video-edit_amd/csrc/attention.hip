@@ -24,7 +24,7 @@
 //     exp2(m_old - m_new) is per lane.
 // K and V tiles reach LDS by direct-to-LDS DMA (double-buffered, the next tile in flight
 // during the current one, one barrier per tile); LDS rows of 256 bytes store 16-byte
-// chunk c at c ^ (row & 15).
+// chunk c at a row-dependent XOR of c (chunk_at, chunk_at_v).
 //
 // ds_read_b64_tr_b16 lane layout (measured on gfx950): within each group of 16
 // lanes, lane a points at 4 consecutive 16-bit values M[a][0..3] and lane i receives
@@ -50,7 +50,13 @@ constexpr int kTileB = kBK * kRowB;    // 16 KB per K or V tile
 template <int J>
 using IC = std::integral_constant<int, J>;
 
+// K tile: 16-byte chunk c of key row r at c ^ (r & 15) -- the fragment reads take 16 consecutive rows of one
+// logical chunk. V tile: c ^ vsw(r) -- a transpose read takes rows 4n..4n+3 and logical chunks 4m..4m+3
+// (32 lanes), which vsw spreads over 16 distinct physical chunks (and over 8 distinct chunk positions mod 8 per
+// 16 lanes), where (r & 15) folded them onto 4.
 __device__ __forceinline__ int chunk_at(int row, int chunk) { return row * kRowB + ((chunk ^ (row & 15)) << 4); }
+__device__ __forceinline__ int vsw(int row) { return ((row & 1) << 2) ^ ((row & 2) ? 10 : 0); }
+__device__ __forceinline__ int chunk_at_v(int row, int chunk) { return row * kRowB + ((chunk ^ vsw(row)) << 4); }
 
 __device__ __forceinline__ v16f mfma_bf16(const bf16x8& a, const bf16x8& b, const v16f& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -110,9 +116,8 @@ __global__ __launch_bounds__(256, QB == 1 ? 2 : 1) void attn_fwd_d128(AttnArgs a
     for (int i = 0; i < 4; ++i) {
       const int row = wave * 16 + i * 4 + (lane >> 4);
       const int64_t key = min(k0 + row, Lk - 1);
-      const int chunk = (lane & 15) ^ (row & 15);
-      kp[i] = kbase + key * a.k.stride_token + chunk * 8;
-      vp[i] = vbase + key * a.v.stride_token + chunk * 8;
+      kp[i] = kbase + key * a.k.stride_token + ((lane & 15) ^ (row & 15)) * 8;
+      vp[i] = vbase + key * a.v.stride_token + ((lane & 15) ^ vsw(row)) * 8;
     }
   };
   auto dma_tile = [&](int buf) {
@@ -252,9 +257,9 @@ __global__ __launch_bounds__(256, QB == 1 ? 2 : 1) void attn_fwd_d128(AttnArgs a
           const int col = db * 32 + tr_col;  // element column (4 consecutive)
           const int chunk = col >> 3, within = (col & 7) * 2;
           const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_s16x4*)(vt + chunk_at(row0, chunk) + within));
+              (lds_s16x4*)(vt + chunk_at_v(row0, chunk) + within));
           const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_s16x4*)(vt + chunk_at(row0 + 8, chunk) + within));
+              (lds_s16x4*)(vt + chunk_at_v(row0 + 8, chunk) + within));
           const v4i va = __builtin_bit_cast(v4i, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
           for (int i = 0; i < QB; ++i) o[i][db] = mfma_bf16(as_bf16x8(va), as_bf16x8(pb[i][2 * kb + b]), o[i][db]);
