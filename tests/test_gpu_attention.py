@@ -43,7 +43,7 @@ def _check(out, q, k, v, what, scale=None, rows=None):
 
 
 @pytest.mark.parametrize("Lq,Lk,H", [(1, 1, 1), (5, 3, 2), (128, 64, 1), (130, 65, 2), (300, 700, 3),
-                                     (257, 129, 4), (64, 1000, 1)])
+                                     (257, 129, 4), (64, 1000, 1), (33, 32, 2), (40, 33, 1), (70, 96, 2)])
 def test_random_shapes(Lq, Lk, H):
     announce("attention random", Lq, Lk, H)
     q, k, v = _inputs(Lq, Lk, H, Lq * 31 + Lk)
@@ -64,16 +64,18 @@ def test_single_key_is_exact():
     assert np.array_equal(u16(_run(q, k, v)), np.broadcast_to(u16(v), (77, 3, 128)))
 
 
-def test_identical_keys_exact_mean():
-    """64 identical keys: every probability is exactly 1, small-integer values sum exactly,
-    so the output is the bf16 rounding of their mean."""
-    announce("attention identical keys")
+@pytest.mark.parametrize("Lk", [64, 40])
+def test_identical_keys_exact_mean(Lk):
+    """Lk identical keys (a full tile; a tile whose second 32-key half is partly past the end):
+    every probability is exactly 1, small-integer values sum exactly, so the output is the bf16
+    rounding of their mean."""
+    announce("attention identical keys", Lk)
     rng = np.random.default_rng(5)
     H = 2
     q = torch.from_numpy(rng.standard_normal((40, H, 128)).astype(np.float32)).to(torch.bfloat16)
-    k = torch.from_numpy(np.repeat(rng.standard_normal((1, H, 128)).astype(np.float32), 64, axis=0)
+    k = torch.from_numpy(np.repeat(rng.standard_normal((1, H, 128)).astype(np.float32), Lk, axis=0)
                          ).to(torch.bfloat16)
-    v = torch.from_numpy(rng.integers(-8, 9, (64, H, 128)).astype(np.float32)).to(torch.bfloat16)
+    v = torch.from_numpy(rng.integers(-8, 9, (Lk, H, 128)).astype(np.float32)).to(torch.bfloat16)
     exp = f32_to_bf16((bf16_to_f32(u16(v)).astype(np.float64).mean(axis=0)).astype(np.float32))
     assert np.array_equal(u16(_run(q, k, v)), np.broadcast_to(exp, (40, H, 128)))
 
