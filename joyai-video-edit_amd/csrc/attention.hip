@@ -44,6 +44,7 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kD = 128;
+constexpr float kMaxSlack = 8.0f;  // see soft_step
 constexpr int kBK = 64;                // keys per tile
 constexpr int kRowB = kD * 2;          // bytes per K / V row
 constexpr int kTileB = kBK * kRowB;    // 16 KB per K or V tile
@@ -160,7 +161,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_d128(AttnArgs a) {
       for (int r = 0; r < 4; ++r) st.m4[r] = fmaxf(fmaxf(s[r], s[r + 4]), fmaxf(s[r + 8], s[r + 12]));
     } else if (step == 1) {
       const float mt = xor32_max(fmaxf(fmaxf(st.m4[0], st.m4[1]), fmaxf(st.m4[2], st.m4[3])));
-      st.m_new = fmaxf(m_run, mt * sl2);
+      // the running max moves only when a score exceeds it by more than kMaxSlack (log2 units):
+      // probabilities then stay below 2^kMaxSlack, and the rescale of O is rare after the first
+      // tiles (the first tile always sets it: m_run starts at -inf)
+      const float m_cand = mt * sl2;
+      st.m_new = m_cand - m_run > kMaxSlack ? m_cand : m_run;
       st.alpha = __builtin_amdgcn_exp2f(m_run - st.m_new);
       st.rs = 0.f;
     } else if (step <= 5) {
