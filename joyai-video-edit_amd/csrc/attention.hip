@@ -39,6 +39,7 @@ namespace joy {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 typedef __attribute__((address_space(3))) void lds_void;
@@ -152,15 +153,19 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_d128(AttnArgs a) {
 
   // softmax of one 32-key half (16 scores per lane) in 8 steps
   struct Soft {
-    float m4[4], m_new, alpha, rs;
-    float p[4];
+    float m, m_new, alpha, rs;
   };
   auto soft_step = [&](int step, const v16f& s, v4i (&pb)[2], Soft& st) {
-    if (step == 0) {
+    if (step == 0) {  // max of 16 scores as a chain of 3-input maxima (v_max3_f32)
+      float m = fmaxf(fmaxf(s[0], s[1]), s[2]);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) st.m4[r] = fmaxf(fmaxf(s[r], s[r + 4]), fmaxf(s[r + 8], s[r + 12]));
+      for (int r = 3; r < 9; r += 2) m = fmaxf(fmaxf(m, s[r]), s[r + 1]);
+      st.m = m;
     } else if (step == 1) {
-      const float mt = xor32_max(fmaxf(fmaxf(st.m4[0], st.m4[1]), fmaxf(st.m4[2], st.m4[3])));
+      float m = st.m;
+#pragma unroll
+      for (int r = 9; r < 15; r += 2) m = fmaxf(fmaxf(m, s[r]), s[r + 1]);
+      const float mt = xor32_max(fmaxf(m, s[15]));
       // the running max moves only when a score exceeds it by more than kMaxSlack (log2 units):
       // probabilities then stay below 2^kMaxSlack, and the rescale of O is rare after the first
       // tiles (the first tile always sets it: m_run starts at -inf)
@@ -169,20 +174,20 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_d128(AttnArgs a) {
       st.alpha = __builtin_amdgcn_exp2f(m_run - st.m_new);
       st.rs = 0.f;
     } else if (step <= 5) {
+      // 4 probabilities: rounded to bf16 pairs for the PV operand, and summed as those bf16 values
+      // (two v_dot2c_f32_bf16 against (1, 1)), so the row sum normalises exactly the weights the
+      // MFMAs apply
       const int r0 = (step - 2) * 4;
       float q[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        q[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r0 + j], sl2, -st.m_new));
-        st.rs += q[j];
-      }
-      if ((r0 & 4) == 0) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) st.p[j] = q[j];
-      } else {
-        pb[r0 >> 3] = (v4i){(int)pack_bf16x2(st.p[0], st.p[1]), (int)pack_bf16x2(st.p[2], st.p[3]),
-                            (int)pack_bf16x2(q[0], q[1]), (int)pack_bf16x2(q[2], q[3])};
-      }
+      for (int j = 0; j < 4; ++j) q[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r0 + j], sl2, -st.m_new));
+      const uint32_t pk0 = pack_bf16x2(q[0], q[1]), pk1 = pack_bf16x2(q[2], q[3]);
+      const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+      st.rs = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk0), one, st.rs, false);
+      st.rs = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk1), one, st.rs, false);
+      const int h = (r0 >> 2) & 1;
+      pb[r0 >> 3][2 * h] = (int)pk0;
+      pb[r0 >> 3][2 * h + 1] = (int)pk1;
     } else if (step == 6) {
       st.rs = xor32_sum(st.rs);
       l_run = l_run * st.alpha + st.rs;
