@@ -1081,19 +1081,6 @@ ResidualArgs residual_args(const GemmArgs& g) {
   return ResidualArgs{(const uint16_t*)g.residual, g.ldr, (const uint16_t*)g.gate};
 }
 
-// Number of compute units of the current device (cached per device).
-int device_cus() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-      cus = 256;
-    cached[dev] = cus;
-  }
-  return cached[dev];
-}
 
 // Full rounds of 256x256 tiles (one workgroup per CU), then the remaining tiles of
 // the last, partial round split into 4 (128x128) or 2 (256x128) sub-tiles so that

@@ -125,4 +125,9 @@ hipError_t launch_joint_qkv_pack(const JointPackArgs& a, hipStream_t st);
 hipError_t launch_cached_kv_pack(const CachedPackArgs& a, hipStream_t st);
 hipError_t launch_attention_fwd(const AttnArgs& a, hipStream_t st);
 
+// Compute units of the current device, and workgroups of `threads` threads of `kern` that
+// stay resident per CU (HIP occupancy API, at least 1); both cached (device_info.hip).
+int device_cus();
+int resident_blocks(const void* kern, int threads);
+
 }  // namespace joy

@@ -465,38 +465,6 @@ __global__ __launch_bounds__(256) void norm_mod_scalar(NormModArgs a) {
   }
 }
 
-// Workgroups of `threads` threads of `kern` resident per CU (HIP occupancy API,
-// cached per kernel and block size; at least 1).
-int resident_blocks(const void* kern, int threads) {
-  static const void* cached_kern[16];
-  static int cached_threads[16], cached_blocks[16], n_cached = 0;
-  for (int i = 0; i < n_cached; ++i)
-    if (cached_kern[i] == kern && cached_threads[i] == threads) return cached_blocks[i];
-  int blocks = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kern, threads, 0) != hipSuccess || blocks < 1)
-    blocks = 1;
-  if (n_cached < 16) {
-    cached_kern[n_cached] = kern;
-    cached_threads[n_cached] = threads;
-    cached_blocks[n_cached] = blocks;
-    ++n_cached;
-  }
-  return blocks;
-}
-
-int device_cus() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-      cus = 256;
-    cached[dev] = cus;
-  }
-  return cached[dev];
-}
-
 template <int DT, int NORM, bool kFp8, bool kDivide>
 hipError_t launch_dt(const NormModArgs& a, hipStream_t st) {
   const dim3 block(256);

@@ -118,3 +118,30 @@ def test_nonfinite_rows_follow_torch():
     # finite rows exact; rows with inf: scale inf, finite elements -> 0, inf -> NaN code
     assert np.array_equal(q[[0, 3]], qr[[0, 3]])
     assert np.array_equal(q[1] & 0x7F, qr[1] & 0x7F) and np.array_equal(q[2] & 0x7F, qr[2] & 0x7F)
+
+
+# Row counts above what one round of resident waves holds (every row checked), for
+# 1, 2, 2 ragged, 4, 8, 12 and 16 vectors per lane.
+@pytest.mark.parametrize("M,K", [(9000, 512), (9000, 1024), (9001, 1000), (8000, 2048), (5000, 4096),
+                                 (3500, 5120), (2500, 8192)])
+def test_many_rows_every_row(M, K):
+    announce("quant many rows", M, K)
+    x = outlier_acts(M, K, gen(M ^ K))
+    check(x, "div")
+    check(x.to(torch.float16), "rcp")
+
+
+def test_many_rows_nonfinite_rows():
+    announce("quant many rows, inf rows")
+    M, K = 9000, 1024
+    x = outlier_acts(M, K, gen(11))
+    bad = [17, 4500, 8999]
+    x[17, 3] = float("inf")
+    x[4500, 1000] = float("-inf")
+    x[8999, 0] = float("nan")
+    q, s = run_quant(x, True)
+    qr, sr = oq.quant_per_token(u16(x), "bf16", "div")
+    good = np.setdiff1d(np.arange(M), bad)
+    assert np.array_equal(s[good], sr[good]) and np.array_equal(q[good], qr[good])
+    assert np.isinf(s[17]) and np.isinf(s[4500]) and np.isnan(s[8999])
+    assert np.array_equal(q[bad] & 0x7F, qr[bad] & 0x7F)
