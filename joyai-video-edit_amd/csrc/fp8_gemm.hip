@@ -1308,17 +1308,20 @@ hipError_t launch_gemm_t(const GemmArgs& g, hipStream_t st) {
                     (!g.residual || ((uintptr_t)g.residual % 16 == 0 && g.ldr % 8 == 0 &&
                                      (uintptr_t)g.gate % 16 == 0));
   if (fast && g.M <= kSmallMaxM) return launch_small_m<kBf16, kEpi>(g, st);
-  if (fast && g.M <= 2048 && g.K >= 8192 && g.K % 128 == 0) {
-    // Long K with less than one round of 256x256 tiles (the reference's 16384-wide
-    // FFN-down at 1024 / 1560 tokens): deep-K 128-row tiles. Measured with W from HBM:
+  if (fast && g.M <= 2048 && g.K >= 4096 && g.K % 128 == 0) {
+    // Less than one round of 256x256 tiles: deep-K 128-row tiles. Measured with W
+    // from HBM, long K (the reference's 16384-wide FFN-down at 1024 / 1560 tokens):
     // 1024 x 16384 x 4096: 79.3 us vs 89.3 (256x256 + split tail); 1560 x 16384 x 4096:
-    // 140.3 us vs 151.7.
+    // 140.3 us vs 151.7. At K 4096 only where the 128-row tiles fit one round:
+    // 1024 x 4096 x 4096 26.9 us vs 30.1, 1560 x 4096 x 4096 42.6 vs 44.2, while
+    // 1024 x 4096 x 12288 (1.5 rounds of 128x256) takes 82.5 us vs 66.6.
     const int P = device_cus();
     const int64_t t256 = (int64_t)((g.M + 255) / 256) * ((g.N + 255) / 256);
     const int64_t t128 = (int64_t)((g.M + 127) / 128) * ((g.N + 127) / 128);
+    const int64_t t128x256 = (int64_t)((g.M + 127) / 128) * ((g.N + 255) / 256);
     if (t256 < P) {
       if (t128 <= P) return launch_deepk<kBf16, kEpi, 128, 128, 128, 3, 3>(g, 1, nullptr, st);
-      return launch_deepk<kBf16, kEpi, 128, 256, 128, 2, 3>(g, 1, nullptr, st);
+      if (g.K >= 8192 || t128x256 <= P) return launch_deepk<kBf16, kEpi, 128, 256, 128, 2, 3>(g, 1, nullptr, st);
     }
   }
   if (fast) return launch_4w<kBf16, kEpi>(g, st);
