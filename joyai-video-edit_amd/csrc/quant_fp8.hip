@@ -145,11 +145,14 @@ __global__ __launch_bounds__(256) void quant_rows_vec(const uint4* __restrict__ 
     for (int i = 0; i < VPT; ++i) {
       const int idx = lane + i * kWave;
       if (idx < nvec) {
+        // No clamp needed on rows with a finite scale: |x| <= absmax, so the scaled value is at
+        // most 448 * (1 + 2^-23) (448.00003 for 15 % of the bf16 absmax values, both roundings),
+        // below 464, the midpoint to the next e4m3 step, so the conversion rounds it to 448.
         float f[8];
         unpack8<kFp16, true>(v[i], f);
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-          f[j] = __builtin_amdgcn_fmed3f(scale_value<kDivide>(f[j], s, r), -kFp8Max, kFp8Max);
+          f[j] = scale_value<kDivide>(f[j], s, r);
         uint2 o;
         o.x = pack_fp8x4(f[0], f[1], f[2], f[3]);
         o.y = pack_fp8x4(f[4], f[5], f[6], f[7]);
