@@ -130,3 +130,22 @@ def test_device_division_formula_exhaustive(is_fp16):
     pairs = sum(r[1] for r in res)
     assert pairs > 9e8
     assert bad == 0, [r for r in res if r[0]][:1]
+
+
+def test_scaled_absmax_stays_below_the_rounding_midpoint():
+    """The device quantiser converts x / s (or x * (1 / s)) without clamping on rows
+    with a finite scale. That equals clamp-then-cast only if the scaled absmax never
+    reaches 464, the midpoint between 448 and the next e4m3 step: checked over every
+    positive finite bf16 and fp16 absmax, both roundings (division emulated as the
+    kernel does it: reciprocal, two FMAs)."""
+    bf = (np.arange(1, 0x7F80, dtype=np.uint32) << 16).view(np.float32)
+    fp = np.arange(1, 0x7C00, dtype=np.uint16).view(np.float16).astype(np.float32)
+    for amax in (bf, fp):
+        s = (np.maximum(amax, np.float32(1e-8)) / np.float32(448)).astype(np.float32)
+        r = (np.float32(1) / s).astype(np.float32)
+        q0 = (amax * r).astype(np.float32)
+        e = (-q0.astype(np.float64) * s + amax).astype(np.float32)
+        q1 = (e.astype(np.float64) * r + q0).astype(np.float32)
+        for v in (q0, q1):
+            assert v.max() < 464.0 and v.max() <= np.float32(448) * (1 + 2.0 ** -22)
+        assert (q0 > 448).any()  # the bound is reached: the conversion's rounding does the clamp
