@@ -108,67 +108,103 @@ def _rms_two_round(x, w, eps):
 
 
 def double_stream_block(img, txt, vec, streams, heads, img_cos_half, img_sin_half, cached=(),
-                        division_min_k=8192, eps=1e-6):
+                        division_min_k=8192, eps=1e-6, skip_text_stream=False, write_only=False,
+                        cache_tokens=None, cache_pre_rope=True, out_rows=None):
     """The quantised block chain on the CPU, with the reference's numerics at every step.
 
     img [L, E], txt [T, E], vec [1, E] bf16; ``streams`` = (img_w, txt_w) dicts with bf16
     ``mod_table`` [1, 6, E], ``q_norm``/``k_norm`` [D] and per linear ``<name>_q`` [N, K] e4m3fn,
     ``<name>_s`` [N] fp32, ``<name>_b`` [N] bf16 for qkv, proj, up, down; ``cached`` = list of
-    (key_pre_rope [len, H, D] bf16, value [len, H, D] bf16, cos_full [len, D] f32, sin_full).
-    Returns (img_out, txt_out, k_pre_img, v_img).
+    (key [len, H, D] bf16, value [len, H, D] bf16, cos_full [len, D] f32, sin_full): a key
+    stored before RoPE is rotated with its tables; with ``cos_full`` None it was stored rotated
+    and is used as is (``_concat_kv_entries``, dit.py:216-271).
+
+    Modes of ``MMDoubleStreamBlock.forward`` (dit.py:360-558): ``skip_text_stream`` attends
+    over [cached | video] and leaves txt unchanged (dit.py:481-487,500-506); ``write_only``
+    returns right after the cache write (dit.py:446-459); ``cache_tokens`` keeps the first
+    tokens only (``kv_cache_write_seq_len``, dit.py:449-451); ``cache_pre_rope`` False keeps
+    the rotated K (dit.py:432-433).
+    ``out_rows`` = (img_rows, txt_rows) index tensors: every K / V row is still computed, but the
+    attention and the row-local tail only for those output rows (the full-size check samples rows).
+    Returns (img_out, txt_out, k_cache, v_cache) (img_out / txt_out: the selected rows).
     """
     L, E = img.shape
     T = txt.shape[0]
     D = E // heads
-    outs = {}
-    qkvs = []
-    for x, w in ((img, streams[0]), (txt, streams[1])):
-        mod = [c.squeeze(1) for c in (w["mod_table"].float() + vec.float().unsqueeze(1)).to(torch.bfloat16)
-               .chunk(6, dim=1)]
-        xm = _layernorm_modulate_ref(x, mod[0], mod[1], eps)
-        qkv = _fp8_linear_ref(xm, w["qkv_q"], w["qkv_s"], w["qkv_b"], E >= division_min_k)
-        qkvs.append((qkv, mod))
-    # video: q/k RMSNorm (one rounding) + RoPE; pre-RoPE K kept
-    qkv_i = qkvs[0][0].view(L, 3, heads, D)
+    n_cache = L if cache_tokens is None else int(cache_tokens)
     wi, wt = streams
+
+    def modulation(w):
+        # ModulateWan (dit.py:97-111): table + vec, six chunks
+        return [c.squeeze(1) for c in (w["mod_table"].float() + vec.float().unsqueeze(1)).to(torch.bfloat16)
+                .chunk(6, dim=1)]
+
+    def qkv_proj(x, w, mod):
+        xm = _layernorm_modulate_ref(x, mod[0], mod[1], eps)
+        return _fp8_linear_ref(xm, w["qkv_q"], w["qkv_s"], w["qkv_b"], E >= division_min_k)
+
+    mod_i = modulation(wi)
+    qkv_i = qkv_proj(img, wi, mod_i).view(L, 3, heads, D)
     qi, ki, vi = qkv_i[:, 0], qkv_i[:, 1], qkv_i[:, 2]
 
     def norm1(x, wn):
         xf = x.float()
         return xf * torch.rsqrt(xf.square().mean(-1, keepdim=True) + eps) * wn.float()
 
+    # video: q/k RMSNorm (one rounding) + RoPE; pre-RoPE K kept
     qh, kh = norm1(qi, wi["q_norm"]), norm1(ki, wi["k_norm"])
     q_img = _rope_half(qh, img_cos_half, img_sin_half).to(torch.bfloat16)
     k_img = _rope_half(kh, img_cos_half, img_sin_half).to(torch.bfloat16)
-    k_pre = kh.to(torch.bfloat16)
-    # condition: two-rounding q/k RMSNorm, no RoPE (fused_joint_qkv_pack.cu:58-79)
-    qkv_t = qkvs[1][0].view(T, 3, heads, D)
-    q_txt = _rms_two_round(qkv_t[:, 0], wt["q_norm"], eps)
-    k_txt = _rms_two_round(qkv_t[:, 1], wt["k_norm"], eps)
-    # cached chunks rotated with fp32 full-width tables (fused_joint_qkv_pack.cu:207-218)
+    k_cache = (kh.to(torch.bfloat16) if cache_pre_rope else k_img)[:n_cache]
+    v_cache = vi[:n_cache].contiguous()
+    if write_only:
+        return img, txt, k_cache, v_cache
+
+    if not skip_text_stream:
+        mod_t = modulation(wt)
+        # condition: two-rounding q/k RMSNorm, no RoPE (fused_joint_qkv_pack.cu:58-79)
+        qkv_t = qkv_proj(txt, wt, mod_t).view(T, 3, heads, D)
+        q_txt = _rms_two_round(qkv_t[:, 0], wt["q_norm"], eps)
+        k_txt = _rms_two_round(qkv_t[:, 1], wt["k_norm"], eps)
+    # cached chunks: pre-RoPE keys rotated with fp32 full-width tables (fused_joint_qkv_pack.cu:207-218)
     ck, cv = [], []
     for key, value, cos, sin in cached:
-        kf = key.float()
-        c = cos.float()[:, None, 0::2]
-        s = sin.float()[:, None, 0::2]
-        out = torch.empty_like(kf)
-        out[..., 0::2] = kf[..., 0::2] * c - kf[..., 1::2] * s
-        out[..., 1::2] = kf[..., 0::2] * s + kf[..., 1::2] * c
-        ck.append(out.to(torch.bfloat16))
+        if cos is None:
+            ck.append(key)
+        else:
+            kf = key.float()
+            c = cos.float()[:, None, 0::2]
+            s = sin.float()[:, None, 0::2]
+            out = torch.empty_like(kf)
+            out[..., 0::2] = kf[..., 0::2] * c - kf[..., 1::2] * s
+            out[..., 1::2] = kf[..., 0::2] * s + kf[..., 1::2] * c
+            ck.append(out.to(torch.bfloat16))
         cv.append(value)
-    Q = torch.cat([q_img, q_txt])
-    K = torch.cat(ck + [k_img, k_txt])
-    V = torch.cat(cv + [vi, qkv_t[:, 2]])
+    if skip_text_stream:
+        Q, K, V = q_img, torch.cat(ck + [k_img]), torch.cat(cv + [vi])
+    else:
+        Q = torch.cat([q_img, q_txt])
+        K = torch.cat(ck + [k_img, k_txt])
+        V = torch.cat(cv + [vi, qkv_t[:, 2]])
+    ri = torch.arange(L) if out_rows is None else out_rows[0]
+    rt = torch.arange(T) if out_rows is None else out_rows[1]
+    sel = ri if skip_text_stream else torch.cat([ri, L + rt])
+    Q = Q[sel]
     attn = torch.nn.functional.scaled_dot_product_attention(
         Q.float().transpose(0, 1)[None], K.float().transpose(0, 1)[None], V.float().transpose(0, 1)[None])
-    attn = attn[0].transpose(0, 1).reshape(L + T, E).to(torch.bfloat16)
-    res = []
-    for (x, w, (qkv, mod), a) in ((img, wi, qkvs[0], attn[:L]), (txt, wt, qkvs[1], attn[L:])):
+    attn = attn[0].transpose(0, 1).reshape(Q.shape[0], E).to(torch.bfloat16)
+    n_i = ri.numel()
+
+    def mlp_tail(x, w, mod, a):
         p = _fp8_linear_ref(a, w["proj_q"], w["proj_s"], w["proj_b"], E >= division_min_k)
         x = (x.float() + p.float() * mod[2].float()).to(torch.bfloat16)
         xm = _layernorm_modulate_ref(x, mod[3], mod[4], eps)
         h = _fp8_linear_ref(xm, w["up_q"], w["up_s"], w["up_b"], E >= division_min_k, gelu=True)
         d = _fp8_linear_ref(h, w["down_q"], w["down_s"], w["down_b"], h.shape[1] >= division_min_k)
-        x = (x.float() + d.float() * mod[5].float()).to(torch.bfloat16)
-        res.append(x)
-    return res[0], res[1], k_pre, vi.contiguous()
+        return (x.float() + d.float() * mod[5].float()).to(torch.bfloat16)
+
+    img_out = mlp_tail(img[ri], wi, mod_i, attn[:n_i])
+    txt_out = txt[rt] if skip_text_stream else mlp_tail(txt[rt], wt, mod_t, attn[n_i:])
+    if out_rows is None and skip_text_stream:
+        txt_out = txt
+    return img_out, txt_out, k_cache, v_cache
