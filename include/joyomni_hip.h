@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define JOY_ABI_VERSION 7
+#define JOY_ABI_VERSION 8
 
 #if defined(__GNUC__) || defined(__clang__)
 #define JOY_API __attribute__((visibility("default")))
@@ -148,11 +148,16 @@ JOY_API joy_status joy_fused_qk_norm_rope_3d_paired(void *q, void *k, int64_t ba
  *   the cache write of pre-RoPE K and compact V                   deploy/xvideo/models/dit/dit.py:446-451,867-882
  * qkv: bf16 [seq_len, 3*num_heads*head_dim] with row stride qkv_row_stride (elements).
  * q_out, k_out, v_out: bf16 [seq_len, num_heads, head_dim] with token strides (elements);
- *   k_out and v_out may be NULL. v_out receives V itself (e.g. the video rows of the
+ *   each may be NULL (q_out NULL: Q is not read, as in the reference's cache-only
+ *   forward, dit.py:446-459). v_out receives V itself (e.g. the video rows of the
  *   joint attention V, dit.py:489-496), so the joint pack need not copy them.
  * cache_k, cache_v: bf16 rings [num_slots, slot_capacity, num_heads, head_dim]
- *   (either both NULL or both set); tokens go to rows slot_offset .. slot_offset+seq_len-1
- *   of slot `slot`: cache_k gets the normalised pre-RoPE K, cache_v a copy of V.
+ *   (either both NULL or both set). The first cache_tokens tokens (0 <= cache_tokens
+ *   <= seq_len; kv_cache_write_seq_len of dit.py:449-451, e.g. the current chunk
+ *   without its ref-video tokens) go to rows slot_offset .. slot_offset+cache_tokens-1
+ *   of slot `slot`: cache_v gets a copy of V; cache_k gets the normalised K before
+ *   rotation (cache_post_rope == 0, kv_cache_pre_rope=True) or the rotated K
+ *   (cache_post_rope != 0, the reference's default post-RoPE cache, dit.py:432-433).
  */
 JOY_API joy_status joy_fused_qkv_norm_rope_cache(const void *qkv, int64_t qkv_row_stride, int64_t seq_len,
                                          int64_t num_heads, int64_t head_dim, float eps,
@@ -162,7 +167,7 @@ JOY_API joy_status joy_fused_qkv_norm_rope_cache(const void *qkv, int64_t qkv_ro
                                          void *v_out, int64_t v_out_stride,
                                          void *cache_k, void *cache_v, int64_t num_slots,
                                          int64_t slot_capacity, int64_t slot, int64_t slot_offset,
-                                         void *stream);
+                                         int64_t cache_tokens, int cache_post_rope, void *stream);
 
 /*
  * A bf16 [len, num_heads, head_dim] view with a dense last dimension: element

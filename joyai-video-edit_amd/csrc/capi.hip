@@ -177,6 +177,8 @@ joy_status joy_fused_qk_norm_rope_3d_paired(void* q, void* k, int64_t batch, int
   a.sin = (const uint16_t*)sin;
   a.n_tokens = batch * seq_len;
   a.table_len = seq_len;
+  a.cache_tokens = batch * seq_len;  // k_pre_rope (if given) for every token
+  a.cache_post_rope = false;
   a.num_heads = (int)num_heads;
   a.eps = eps;
   return hip_status(joy::launch_qk_norm_rope(a, (int)head_dim, (hipStream_t)stream),
@@ -191,14 +193,14 @@ joy_status joy_fused_qkv_norm_rope_cache(const void* qkv, int64_t qkv_row_stride
                                          void* v_out, int64_t v_out_stride,
                                          void* cache_k, void* cache_v, int64_t num_slots,
                                          int64_t slot_capacity, int64_t slot, int64_t slot_offset,
-                                         void* stream) {
+                                         int64_t cache_tokens, int cache_post_rope, void* stream) {
   if (seq_len < 0 || num_heads < 0) return fail(JOY_ERR_INVALID_ARGUMENT, "seq_len and num_heads must be >= 0");
   if (head_dim != 64 && head_dim != 128 && head_dim != 256)
     return fail(JOY_ERR_INVALID_ARGUMENT, "Unsupported head_dim: %lld", (long long)head_dim);
   if (num_heads > 0x7fffffffLL) return fail(JOY_ERR_UNSUPPORTED, "num_heads too large");
   const int64_t E = num_heads * head_dim;
   if (qkv_row_stride < 3 * E) return fail(JOY_ERR_INVALID_ARGUMENT, "qkv row stride must be >= 3*num_heads*head_dim");
-  if (q_out_stride < E || (k_out && k_out_stride < E) || (v_out && v_out_stride < E))
+  if ((q_out && q_out_stride < E) || (k_out && k_out_stride < E) || (v_out && v_out_stride < E))
     return fail(JOY_ERR_INVALID_ARGUMENT, "q_out/k_out/v_out token stride must be >= num_heads*head_dim");
   if ((cache_k == nullptr) != (cache_v == nullptr))
     return fail(JOY_ERR_INVALID_ARGUMENT, "cache_k and cache_v must be provided together");
@@ -208,26 +210,30 @@ joy_status joy_fused_qkv_norm_rope_cache(const void* qkv, int64_t qkv_row_stride
     if (slot < 0 || slot >= num_slots)
       return fail(JOY_ERR_INVALID_ARGUMENT, "slot %lld out of range [0, %lld)", (long long)slot,
                   (long long)num_slots);
-    if (slot_offset < 0 || slot_offset + seq_len > slot_capacity)
+    if (cache_tokens < 0 || cache_tokens > seq_len)
+      return fail(JOY_ERR_INVALID_ARGUMENT, "cache_tokens %lld out of range [0, seq_len = %lld]",
+                  (long long)cache_tokens, (long long)seq_len);
+    if (slot_offset < 0 || slot_offset + cache_tokens > slot_capacity)
       return fail(JOY_ERR_INVALID_ARGUMENT, "tokens [%lld, %lld) do not fit a slot of %lld tokens",
-                  (long long)slot_offset, (long long)(slot_offset + seq_len), (long long)slot_capacity);
+                  (long long)slot_offset, (long long)(slot_offset + cache_tokens), (long long)slot_capacity);
   }
+  if (!q_out && !k_out && !v_out && !cache_k) return ok();  // nothing to write
   if (seq_len == 0 || num_heads == 0) return ok();
   if (seq_len * num_heads > kMaxUnits)
     return fail(JOY_ERR_UNSUPPORTED, "seq_len*num_heads above 2^31 - 2^20");
-  if (!qkv || !q_out || !q_weight || !k_weight || !cos || !sin)
-    return fail(JOY_ERR_INVALID_ARGUMENT, "qkv, q_out, weights and cos/sin must be non-null");
-  if ((qkv_row_stride % 8) || (q_out_stride % 8) || (k_out && (k_out_stride % 8)) ||
+  if (!qkv || !q_weight || !k_weight || !cos || !sin)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "qkv, weights and cos/sin must be non-null");
+  if ((qkv_row_stride % 8) || (q_out && (q_out_stride % 8)) || (k_out && (k_out_stride % 8)) ||
       (v_out && (v_out_stride % 8)))
     return fail(JOY_ERR_UNSUPPORTED, "token strides must be multiples of 8 elements");
-  if (!aligned(qkv, 16) || !aligned(q_out, 16) || (k_out && !aligned(k_out, 16)) ||
+  if (!aligned(qkv, 16) || (q_out && !aligned(q_out, 16)) || (k_out && !aligned(k_out, 16)) ||
       (v_out && !aligned(v_out, 16)) ||
       (cache_k && (!aligned(cache_k, 16) || !aligned(cache_v, 16))) || !aligned(q_weight, 16) ||
       !aligned(k_weight, 16) || !aligned(cos, 8) || !aligned(sin, 8))
     return fail(JOY_ERR_UNSUPPORTED, "tensors must be 16-byte aligned (cos/sin 8-byte)");
   const uint16_t* base = (const uint16_t*)qkv;
   joy::NormRopeArgs a;
-  a.q_in = base;
+  a.q_in = q_out ? base : nullptr;
   a.k_in = base + E;
   a.v_in = (cache_v || v_out) ? base + 2 * E : nullptr;
   a.in_stride = qkv_row_stride;
@@ -248,6 +254,8 @@ joy_status joy_fused_qkv_norm_rope_cache(const void* qkv, int64_t qkv_row_stride
   a.sin = (const uint16_t*)sin;
   a.n_tokens = seq_len;
   a.table_len = seq_len;
+  a.cache_tokens = cache_k ? cache_tokens : 0;
+  a.cache_post_rope = cache_post_rope != 0;
   a.num_heads = (int)num_heads;
   a.eps = eps;
   return hip_status(joy::launch_qk_norm_rope(a, (int)head_dim, (hipStream_t)stream),

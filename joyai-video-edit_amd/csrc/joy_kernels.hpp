@@ -8,7 +8,7 @@ namespace joy {
 
 // Token-strided [tokens, H, D] bf16 views (strides in elements per token).
 struct NormRopeArgs {
-  const uint16_t* q_in;
+  const uint16_t* q_in;  // null: Q is neither read nor written
   const uint16_t* k_in;
   const uint16_t* v_in;  // may be null
   int64_t in_stride;
@@ -28,6 +28,8 @@ struct NormRopeArgs {
   const uint16_t* sin;
   int64_t n_tokens;   // tokens processed (B * L)
   int64_t table_len;  // cos/sin row = token % table_len
+  int64_t cache_tokens;  // kpre_out / v_out are written for tokens < cache_tokens
+  bool cache_post_rope;  // kpre_out receives the rotated K instead of the normalised K
   int num_heads;
   float eps;
 };

@@ -12,8 +12,9 @@
 //    contiguous [B, L*H, D] tensors, outputs over the inputs);
 //  * the fused op: q, k, v read straight from the QKV GEMM output row
 //    [q(H*D) | k(H*D) | v(H*D)], roped q/k written to the attention operands,
-//    the pre-RoPE k and v written into a slot of the KV ring and, optionally, v
-//    also into the attention V operand.
+//    the pre-RoPE (or rotated) k and v of the first cache_tokens tokens written
+//    into a slot of the KV ring and, optionally, v also into the attention V
+//    operand. Without a q output, q is not read (cache-only forward).
 // Every pointer is a token-strided [tokens, H, D] view, so outputs can land in
 // any caller-owned buffer (ring slot, joint attention buffer) with no copy.
 //
@@ -90,7 +91,7 @@ __global__ __launch_bounds__(512) void qk_norm_rope_kernel(NormRopeArgs a) {
     token[r] = u / a.num_heads;
     hoff[r] = (u - token[r] * a.num_heads) * D + li * 8;
     const int64_t in = (int64_t)token[r] * a.in_stride + hoff[r];
-    qv[r] = ld16<NT>(a.q_in + in);
+    qv[r] = a.q_in ? ld16<NT>(a.q_in + in) : make_uint4(0, 0, 0, 0);
     kv[r] = ld16<NT>(a.k_in + in);
     if (a.v_in) vv[r] = ld16<NT>(a.v_in + in);
     const int64_t trow = (int64_t)(token[r] % a.table_len) * (D / 2) + li * 4;
@@ -136,10 +137,13 @@ __global__ __launch_bounds__(512) void qk_norm_rope_kernel(NormRopeArgs a) {
     }
     if (!valid[r]) continue;
     const int64_t t = token[r];
-    st16<NT>(a.q_out + t * a.q_out_stride + hoff[r], pack_bf16x8(qo));
+    if (a.q_in) st16<NT>(a.q_out + t * a.q_out_stride + hoff[r], pack_bf16x8(qo));
     if (a.k_out) st16<NT>(a.k_out + t * a.k_out_stride + hoff[r], pack_bf16x8(ko));
-    if (a.kpre_out) st16<NT>(a.kpre_out + t * a.kpre_stride + hoff[r], pack_bf16x8(k));
-    if (a.v_out) st16<NT>(a.v_out + t * a.v_out_stride + hoff[r], vv[r]);
+    if (t < a.cache_tokens) {
+      if (a.kpre_out)
+        st16<NT>(a.kpre_out + t * a.kpre_stride + hoff[r], pack_bf16x8(a.cache_post_rope ? ko : k));
+      if (a.v_out) st16<NT>(a.v_out + t * a.v_out_stride + hoff[r], vv[r]);
+    }
     if (a.v_out2) st16<NT>(a.v_out2 + t * a.v_out2_stride + hoff[r], vv[r]);
   }
 }

@@ -92,8 +92,9 @@ _lib_def.define(
     "Tensor(c!)? out, bool exact_division) -> ()")
 _lib_def.define(
     "fused_qkv_norm_rope_cache(Tensor qkv, int num_heads, float eps, Tensor q_weight, "
-    "Tensor k_weight, Tensor cos, Tensor sin, Tensor(a!) q_out, Tensor(b!)? k_out, "
-    "Tensor(c!)? cache_k, Tensor(d!)? cache_v, int slot, int slot_offset, Tensor(e!)? v_out=None) -> ()")
+    "Tensor k_weight, Tensor cos, Tensor sin, Tensor(a!)? q_out, Tensor(b!)? k_out, "
+    "Tensor(c!)? cache_k, Tensor(d!)? cache_v, int slot, int slot_offset, Tensor(e!)? v_out=None, "
+    "int cache_tokens=-1, bool cache_pre_rope=True) -> ()")
 _lib_def.define(
     "fused_cached_kv_pack_out(Tensor key0, Tensor value0, Tensor? key1, Tensor? value1, "
     "Tensor cos, Tensor sin, Tensor(a!) out_k, Tensor(b!) out_v) -> ()")
@@ -308,23 +309,30 @@ def _fused_qk_norm_rope_3d_paired_cuda(q, k, seq_len, num_heads, eps, q_weight, 
     _lib.check(_LIB, st)
 
 
-def _token_stride(t: torch.Tensor, H: int, D: int, name: str) -> int:
-    """Token stride of a [L, H, D] (or [1, L, H, D] / [L, H*D]) view with dense heads."""
+def _token_stride(t: torch.Tensor, L: int, H: int, D: int, name: str, device) -> int:
+    """Token stride of an output view of L tokens: [L, H, D], [1, L, H, D] or [L, H*D], dense heads.
+
+    The kernel writes exactly L token rows through this stride, so a view with another
+    token count (a short or mis-sliced output) is rejected before anything is launched."""
+    _check(t.is_cuda and t.device == device, f"{name} must be a CUDA tensor on the device of qkv")
+    _check(t.dtype == torch.bfloat16, f"{name} must be a bf16 CUDA tensor")
     x = t
     if x.dim() == 4:
         _check(x.size(0) == 1, f"{name} batch must be 1")
         x = x[0]
     if x.dim() == 2:
         _check(x.size(1) == H * D and x.stride(1) == 1, f"{name} must have dense rows of H*D")
-        return x.stride(0)
-    _check(x.dim() == 3 and x.size(1) == H and x.size(2) == D, f"{name} must be [L, H, D]")
-    _check(x.stride(2) == 1 and x.stride(1) == D, f"{name} must have dense heads")
-    return x.stride(0)
+    else:
+        _check(x.dim() == 3 and x.size(1) == H and x.size(2) == D, f"{name} must be [L, H, D]")
+        _check(x.stride(2) == 1 and x.stride(1) == D, f"{name} must have dense heads")
+    _check(x.size(0) == L, f"{name} holds {x.size(0)} tokens, expected {L} (the rows of qkv)")
+    return x.stride(0) if L > 1 else H * D
 
 
 @torch.library.impl(_lib_def, "fused_qkv_norm_rope_cache", "CUDA")
 def _fused_qkv_norm_rope_cache_cuda(qkv, num_heads, eps, q_weight, k_weight, cos, sin, q_out,
-                                    k_out, cache_k, cache_v, slot, slot_offset, v_out=None):
+                                    k_out, cache_k, cache_v, slot, slot_offset, v_out=None, cache_tokens=-1,
+                                    cache_pre_rope=True):
     _check(qkv.is_cuda, "qkv must be a CUDA tensor")
     _check(qkv.dtype == torch.bfloat16, f"qkv dtype is {qkv.dtype}, expected torch.bfloat16")
     x = qkv[0] if qkv.dim() == 3 else qkv
@@ -337,29 +345,30 @@ def _fused_qkv_norm_rope_cache_cuda(qkv, num_heads, eps, q_weight, k_weight, cos
     D = E3 // (3 * H)
     for name, t in (("q_weight", q_weight), ("k_weight", k_weight), ("cos", cos), ("sin", sin)):
         _check_input(t, name, torch.bfloat16)
+        _check(t.device == qkv.device, f"{name} must be on the device of qkv")
     _check(q_weight.numel() == D and k_weight.numel() == D, "weight size must match head_dim")
     _check(cos.shape == (L, D // 2) and sin.shape == (L, D // 2),
            "cos/sin shape must be [seq_len, head_dim/2]")
-    q_stride = _token_stride(q_out, H, D, "q_out")
-    k_stride = _token_stride(k_out, H, D, "k_out") if k_out is not None else 0
-    v_stride = _token_stride(v_out, H, D, "v_out") if v_out is not None else 0
-    for name, t in (("q_out", q_out), ("k_out", k_out), ("v_out", v_out), ("cache_k", cache_k),
-                    ("cache_v", cache_v)):
-        if t is not None:
-            _check(t.is_cuda and t.dtype == torch.bfloat16, f"{name} must be a bf16 CUDA tensor")
+    strides = [_token_stride(t, L, H, D, name, qkv.device) if t is not None else 0
+               for name, t in (("q_out", q_out), ("k_out", k_out), ("v_out", v_out))]
     n_slots = cap = 0
     if (cache_k is None) != (cache_v is None):
         raise RuntimeError("cache_k and cache_v must be provided together")
+    n_cache = L if cache_tokens is None or int(cache_tokens) < 0 else int(cache_tokens)
     if cache_k is not None:
+        for name, t in (("cache_k", cache_k), ("cache_v", cache_v)):
+            _check(t.is_cuda and t.device == qkv.device and t.dtype == torch.bfloat16,
+                   f"{name} must be a bf16 CUDA tensor on the device of qkv")
         _check(cache_k.is_contiguous() and cache_v.is_contiguous(), "cache_k/cache_v must be contiguous")
         _check(cache_k.dim() == 4 and cache_k.shape == cache_v.shape
                and cache_k.shape[2:] == (H, D), "cache must be [num_slots, capacity, H, D]")
         n_slots, cap = cache_k.shape[0], cache_k.shape[1]
     with torch.cuda.device(qkv.device):
         st = _LIB.joy_fused_qkv_norm_rope_cache(
-            _ptr(x), x.stride(0), L, H, D, float(eps), _ptr(q_weight), _ptr(k_weight), _ptr(cos),
-            _ptr(sin), _ptr(q_out), q_stride, _ptr(k_out), k_stride, _ptr(v_out), v_stride, _ptr(cache_k),
-            _ptr(cache_v), n_slots, cap, int(slot), int(slot_offset), _stream(qkv))
+            _ptr(x), x.stride(0) if L > 1 else E3, L, H, D, float(eps), _ptr(q_weight), _ptr(k_weight), _ptr(cos),
+            _ptr(sin), _ptr(q_out), strides[0], _ptr(k_out), strides[1], _ptr(v_out), strides[2], _ptr(cache_k),
+            _ptr(cache_v), n_slots, cap, int(slot), int(slot_offset), n_cache, 0 if cache_pre_rope else 1,
+            _stream(qkv))
     _lib.check(_LIB, st)
 
 
@@ -708,7 +717,8 @@ def _fake_fp8_scaled_mm_gated_residual_inplace(mat_a, mat_b, scales_a, scales_b,
 
 @torch.library.register_fake("joyomni_ops::fused_qkv_norm_rope_cache")
 def _fake_fused_qkv_norm_rope_cache(qkv, num_heads, eps, q_weight, k_weight, cos, sin, q_out,
-                                    k_out, cache_k, cache_v, slot, slot_offset, v_out=None):
+                                    k_out, cache_k, cache_v, slot, slot_offset, v_out=None, cache_tokens=-1,
+                                    cache_pre_rope=True):
     return None
 
 
@@ -816,11 +826,17 @@ def fp8_scaled_mm_gated_residual(mat_a, mat_b, scales_a, scales_b, residual, gat
 
 
 def fused_qkv_norm_rope_cache(qkv, num_heads, eps, q_weight, k_weight, cos, sin, q_out,
-                              k_out=None, cache_k=None, cache_v=None, slot=0, slot_offset=0, v_out=None):
-    """QKV split + q/k RMSNorm + RoPE in one pass; pre-RoPE K and V land in ring slot `slot`;
-    ``v_out`` (optional) receives V as well, e.g. the video rows of the joint attention V."""
+                              k_out=None, cache_k=None, cache_v=None, slot=0, slot_offset=0, v_out=None,
+                              cache_tokens: int = -1, cache_pre_rope: bool = True):
+    """QKV split + q/k RMSNorm + RoPE in one pass.
+
+    Roped Q / K go to ``q_out`` / ``k_out`` (either may be None; without ``q_out`` Q is not read).
+    The first ``cache_tokens`` tokens (all when negative; ``kv_cache_write_seq_len``) of K and V
+    land in ring slot ``slot`` from row ``slot_offset``: K normalised before rotation when
+    ``cache_pre_rope`` (``kv_cache_pre_rope=True``), else rotated. ``v_out`` (optional) receives V
+    as well, e.g. the video rows of the joint attention V."""
     _ops.fused_qkv_norm_rope_cache(qkv, num_heads, eps, q_weight, k_weight, cos, sin, q_out, k_out,
-                                   cache_k, cache_v, slot, slot_offset, v_out)
+                                   cache_k, cache_v, slot, slot_offset, v_out, cache_tokens, cache_pre_rope)
 
 
 def fused_cached_kv_pack_out(key0, value0, key1, value1, cos, sin, out_k, out_v):

@@ -56,7 +56,7 @@ SIGNATURES = {
         _int, [_vp, _vp, _i64, _i64, _i64, _i64, _f32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "joy_fused_qkv_norm_rope_cache": (
         _int, [_vp, _i64, _i64, _i64, _i64, _f32, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _i64,
-               _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
+               _vp, _vp, _i64, _i64, _i64, _i64, _i64, _int, _vp]),
     "joy_fused_joint_qkv_pack": (
         _int, [_view, _view, _view, _view, _view, _view, _view, _view, _vp, _vp, _f32, _i64, _i64,
                _vp, _vp, _vp, _vp]),
@@ -72,7 +72,7 @@ SIGNATURES = {
                _vp]),
 }
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 
 class JoyError(RuntimeError):

@@ -98,6 +98,8 @@ class KVRing:
         self.k = torch.zeros(slots, capacity, heads, head_dim, dtype=torch.bfloat16, device=device)
         self.v = torch.zeros_like(self.k)
         self.lengths = [0] * slots
+        # per slot: K stored before RoPE (kv_cache_pre_rope=True) or rotated (the reference's default)
+        self.pre_rope = [True] * slots
 
     def key(self, slot: int) -> torch.Tensor:
         return self.k[slot, : self.lengths[slot]][None]
@@ -108,11 +110,13 @@ class KVRing:
 
 @dataclass
 class CachedChunk:
-    """A cached chunk to attend to: its ring slot and the fp32 full-width RoPE tables
-    ``[len, D]`` of its window-relative positions (``dit.py:1196-1217``)."""
+    """A cached chunk to attend to: its ring slot and, for a K stored before RoPE, the fp32
+    full-width RoPE tables ``[len, D]`` of its window-relative positions (``dit.py:1196-1217``).
+    A slot holding rotated K (written with ``kv_cache_pre_rope=False``) takes no tables and is
+    copied as is, as ``_concat_kv_entries`` concatenates such entries (``dit.py:258-271``)."""
     slot: int
-    cos: torch.Tensor
-    sin: torch.Tensor
+    cos: Optional[torch.Tensor] = None
+    sin: Optional[torch.Tensor] = None
 
 
 class QuantizedDoubleStreamBlock:
@@ -151,75 +155,148 @@ class QuantizedDoubleStreamBlock:
         """Attention on [B, S, H, D] operands (dit.py:154-167): [B, S, H, D] out, heads dense."""
         return sdpa_attention(q, k, v)
 
+    # -- argument checks ----------------------------------------------------
+    @staticmethod
+    def check_cache_args(L: int, ring: Optional[KVRing], write_slot: Optional[int], cached: Sequence[CachedChunk],
+                         cache_tokens: int) -> None:
+        """Reject cache arguments that would make the chain read or write the wrong rows."""
+        if (ring is None) and (write_slot is not None or cached):
+            raise ValueError("write_slot and cached chunks need a KV ring")
+        if write_slot is not None:
+            if not 0 <= write_slot < len(ring.lengths):
+                raise ValueError(f"write_slot {write_slot} is not a slot of the ring ({len(ring.lengths)} slots)")
+            if not 0 <= cache_tokens <= L:
+                raise ValueError(f"kv_cache_write_seq_len {cache_tokens} is outside [0, {L}]")
+            if cache_tokens > ring.k.shape[1]:
+                raise ValueError(f"{cache_tokens} tokens do not fit a ring slot of {ring.k.shape[1]}")
+        slots = [c.slot for c in cached]
+        if len(set(slots)) != len(slots):
+            raise ValueError(f"a ring slot is attended twice: {slots}")
+        if write_slot is not None and write_slot in slots:
+            # the write would overwrite the chunk before it is read
+            raise ValueError(f"write_slot {write_slot} is also a cached slot; the chunk would be overwritten "
+                             "before attention reads it")
+        for c in cached:
+            if not 0 <= c.slot < len(ring.lengths):
+                raise ValueError(f"cached slot {c.slot} is not a slot of the ring")
+            n = ring.lengths[c.slot]
+            if n <= 0:
+                raise ValueError(f"cached slot {c.slot} is empty")
+            if ring.pre_rope[c.slot]:
+                if c.cos is None or c.sin is None:
+                    raise ValueError(f"cached slot {c.slot} holds K before RoPE and needs its cos/sin tables")
+                for name, t in (("cos", c.cos), ("sin", c.sin)):
+                    if t.dim() != 2 or t.shape[0] != n:
+                        raise ValueError(f"cached slot {c.slot} holds {n} tokens but its {name} table has "
+                                         f"shape {tuple(t.shape)}; expected [{n}, head_dim]")
+            elif c.cos is not None or c.sin is not None:
+                raise ValueError(f"cached slot {c.slot} holds rotated K; it takes no RoPE tables")
+
     # -- forward ------------------------------------------------------------
+    def _cached_into(self, ring: KVRing, cached: Sequence[CachedChunk], k: torch.Tensor, v: torch.Tensor) -> None:
+        """Cached chunks into the head of the joint K / V: runs of pre-RoPE slots rotated on read, two
+        at a time (``fused_cached_kv_pack_out``); rotated slots copied as they are."""
+        off, i = 0, 0
+        while i < len(cached):
+            c0 = cached[i]
+            n0 = ring.lengths[c0.slot]
+            if not ring.pre_rope[c0.slot]:
+                k[0, off:off + n0].copy_(ring.k[c0.slot, :n0])
+                v[0, off:off + n0].copy_(ring.v[c0.slot, :n0])
+                off, i = off + n0, i + 1
+                continue
+            pair = i + 1 < len(cached) and ring.pre_rope[cached[i + 1].slot]
+            seg = cached[i:i + 2] if pair else [c0]
+            n = sum(ring.lengths[c.slot] for c in seg)
+            cos = torch.cat([c.cos for c in seg]) if pair else c0.cos
+            sin = torch.cat([c.sin for c in seg]) if pair else c0.sin
+            k1 = ring.key(seg[1].slot) if pair else None
+            v1 = ring.value(seg[1].slot) if pair else None
+            fused_cached_kv_pack_out(ring.key(c0.slot), ring.value(c0.slot), k1, v1, cos, sin,
+                                     k[:, off:off + n], v[:, off:off + n])
+            off, i = off + n, i + len(seg)
+
     def forward(self, img: torch.Tensor, txt: torch.Tensor, vec: torch.Tensor, img_cos: torch.Tensor,
                 img_sin: torch.Tensor, ring: Optional[KVRing] = None, write_slot: Optional[int] = None,
-                cached: Sequence[CachedChunk] = (), mark: Optional[Callable[[str], None]] = None
+                cached: Sequence[CachedChunk] = (), mark: Optional[Callable[[str], None]] = None,
+                skip_text_stream: bool = False, kv_cache_write_only: bool = False,
+                kv_cache_write_seq_len: Optional[int] = None, kv_cache_pre_rope: bool = True
                 ) -> Tuple[torch.Tensor, torch.Tensor]:
         """img [1, L, E], txt [1, T, E], vec [1, E] bf16; img_cos/img_sin bf16 half tables [L, D/2].
 
-        Writes the video chunk's pre-RoPE K and V into ``ring`` slot ``write_slot`` (if given) and
-        attends to [cached chunks | video | condition]. ``mark(name)`` is called after each stage
-        (used by the benchmark to place timing events). Returns the updated (img, txt).
+        Writes the first ``kv_cache_write_seq_len`` (default all) video tokens' K and V into ``ring``
+        slot ``write_slot`` (if given) -- K before RoPE when ``kv_cache_pre_rope``, else rotated -- and
+        attends to [cached chunks | video | condition] (``dit.py:489-498``), or to [cached chunks |
+        video] with ``skip_text_stream`` (``dit.py:481-487``; txt is returned unchanged).
+        ``kv_cache_write_only`` returns (img, txt) unchanged right after the ring write
+        (``dit.py:446-459``). ``mark(name)`` is called after each stage (the benchmark places timing
+        events there). Returns the updated (img, txt).
         """
         mark = mark or (lambda name: None)
         E, H, D = self.hidden, self.heads, self.head_dim
         L, T = img.shape[1], txt.shape[1]
+        n_cache = L if kv_cache_write_seq_len is None else int(kv_cache_write_seq_len)
+        self.check_cache_args(L, ring, write_slot, cached, n_cache)
+        if kv_cache_write_only and write_slot is None:
+            raise ValueError("kv_cache_write_only needs a ring and a write_slot")
+        ring_k, ring_v, slot = (ring.k, ring.v, write_slot) if write_slot is not None else (None, None, 0)
         img2, txt2 = img.reshape(L, E), txt.reshape(T, E)
         im = self.modulation(self.img, vec)
-        tm = self.modulation(self.txt, vec)
 
         # QKV projections
         q8, s8 = self.norm_quant(img2, im[0], im[1], E)
         img_qkv = self.img.qkv.gemm(q8, s8)
-        q8, s8 = self.norm_quant(txt2, tm[0], tm[1], E)
-        txt_qkv = self.txt.qkv.gemm(q8, s8)
+        if kv_cache_write_only:
+            # only the ring is written: Q is not read, no attention operand is produced
+            fused_qkv_norm_rope_cache(img_qkv, H, NORM_EPS, self.img.q_norm, self.img.k_norm, img_cos, img_sin,
+                                      None, None, ring_k, ring_v, slot, 0, cache_tokens=n_cache,
+                                      cache_pre_rope=kv_cache_pre_rope)
+            ring.lengths[write_slot], ring.pre_rope[write_slot] = n_cache, kv_cache_pre_rope
+            mark("qkv_norm_rope")
+            return img, txt
+        if not skip_text_stream:
+            tm = self.modulation(self.txt, vec)
+            q8, s8 = self.norm_quant(txt2, tm[0], tm[1], E)
+            txt_qkv = self.txt.qkv.gemm(q8, s8)
         mark("qkv")
 
         # joint attention operands: Q = [video | condition], K, V = [cached | video | condition]
         C = sum(ring.lengths[c.slot] for c in cached) if cached else 0
-        q = torch.empty(1, L + T, H, D, dtype=torch.bfloat16, device=img.device)
-        k = torch.empty(1, C + L + T, H, D, dtype=torch.bfloat16, device=img.device)
+        n_q = L if skip_text_stream else L + T
+        q = torch.empty(1, n_q, H, D, dtype=torch.bfloat16, device=img.device)
+        k = torch.empty(1, C + n_q, H, D, dtype=torch.bfloat16, device=img.device)
         v = torch.empty_like(k)
 
-        # video q/k norm + RoPE into the joint buffers, pre-RoPE K / V into the ring
-        if ring is not None and write_slot is not None:
-            fused_qkv_norm_rope_cache(img_qkv, H, NORM_EPS, self.img.q_norm, self.img.k_norm, img_cos, img_sin,
-                                      q[0, :L], k[0, C:C + L], ring.k, ring.v, write_slot, 0, v_out=v[0, C:C + L])
-            ring.lengths[write_slot] = L
-        else:
-            fused_qkv_norm_rope_cache(img_qkv, H, NORM_EPS, self.img.q_norm, self.img.k_norm, img_cos, img_sin,
-                                      q[0, :L], k[0, C:C + L], None, None, 0, 0, v_out=v[0, C:C + L])
+        # video q/k norm + RoPE into the joint buffers, K / V into the ring
+        fused_qkv_norm_rope_cache(img_qkv, H, NORM_EPS, self.img.q_norm, self.img.k_norm, img_cos, img_sin,
+                                  q[0, :L], k[0, C:C + L], ring_k, ring_v, slot, 0, v_out=v[0, C:C + L],
+                                  cache_tokens=n_cache, cache_pre_rope=kv_cache_pre_rope)
+        if write_slot is not None:
+            ring.lengths[write_slot], ring.pre_rope[write_slot] = n_cache, kv_cache_pre_rope
         mark("qkv_norm_rope")
 
-        # cached chunks rotated on read into the head of K / V (one or two segments per launch)
-        off = 0
-        for i in range(0, len(cached), 2):
-            seg = cached[i:i + 2]
-            n = sum(ring.lengths[c.slot] for c in seg)
-            cos = torch.cat([c.cos for c in seg]) if len(seg) > 1 else seg[0].cos
-            sin = torch.cat([c.sin for c in seg]) if len(seg) > 1 else seg[0].sin
-            k1 = ring.key(seg[1].slot) if len(seg) > 1 else None
-            v1 = ring.value(seg[1].slot) if len(seg) > 1 else None
-            fused_cached_kv_pack_out(ring.key(seg[0].slot), ring.value(seg[0].slot), k1, v1, cos, sin,
-                                     k[:, off:off + n], v[:, off:off + n])
-            off += n
+        self._cached_into(ring, cached, k, v)
         mark("cached_kv")
 
-        # condition stream: two-rounding q/k RMSNorm into the tails of Q / K / V
-        tv = txt_qkv.view(1, T, 3, H, D)
-        fused_text_qkv_pack(tv[:, :, 0], tv[:, :, 1], tv[:, :, 2], self.txt.q_norm, self.txt.k_norm, NORM_EPS,
-                            q[:, L:], k[:, C + L:], v[:, C + L:])
+        if not skip_text_stream:
+            # condition stream: two-rounding q/k RMSNorm into the tails of Q / K / V
+            tv = txt_qkv.view(1, T, 3, H, D)
+            fused_text_qkv_pack(tv[:, :, 0], tv[:, :, 1], tv[:, :, 2], self.txt.q_norm, self.txt.k_norm, NORM_EPS,
+                                q[:, L:], k[:, C + L:], v[:, C + L:])
         mark("joint_pack")
         attn = self.attention(q, k, v).flatten(2, 3)
         mark("attention")
 
+        streams = [(img2, self.img, im, attn[0, :L])]
+        if not skip_text_stream:
+            streams.append((txt2, self.txt, tm, attn[0, L:]))
         outs = []
-        for x2d, w, m, a in ((img2, self.img, im, attn[0, :L]), (txt2, self.txt, tm, attn[0, L:])):
+        for x2d, w, m, a in streams:
             x = w.proj.gated_residual(a, x2d, m[2])            # new tensor: the caller's input stays
             q8, s8 = self.norm_quant(x, m[3], m[4], E)
             h = w.up.gemm(q8, s8)
             w.down.gated_residual(h, x, m[5], inplace=True)
             outs.append(x)
         mark("proj_ffn")
-        return outs[0].reshape(1, L, E), outs[1].reshape(1, T, E)
+        txt_out = txt if skip_text_stream else outs[1].reshape(1, T, E)
+        return outs[0].reshape(1, L, E), txt_out

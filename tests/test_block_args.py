@@ -1,0 +1,70 @@
+"""Cache-argument checks of the block chain, on the CPU (no kernel is reached): a write slot
+that is also read, cached tables that disagree with the slot's length, empty slots, rotated
+slots given tables, and write lengths that do not fit."""
+import pytest
+import torch
+
+from joyomni_ops.dit_block import CachedChunk, KVRing, QuantizedDoubleStreamBlock
+
+check = QuantizedDoubleStreamBlock.check_cache_args
+
+
+def _ring():
+    r = KVRing(4, 32, 2, 128, "cpu")
+    r.lengths = [16, 32, 0, 8]
+    return r
+
+
+def _tables(n):
+    return torch.ones(n, 128), torch.zeros(n, 128)
+
+
+def test_valid_arguments_pass():
+    r = _ring()
+    check(24, r, 2, [CachedChunk(0, *_tables(16)), CachedChunk(1, *_tables(32))], 24)
+    check(24, r, None, [CachedChunk(3, *_tables(8))], 24)
+    check(24, None, None, [], 24)
+    r.pre_rope[3] = False
+    check(24, r, 2, [CachedChunk(3)], 10)
+
+
+def test_write_slot_that_is_also_read_is_rejected():
+    r = _ring()
+    with pytest.raises(ValueError, match="write_slot 0 is also a cached slot"):
+        check(24, r, 0, [CachedChunk(0, *_tables(16))], 24)
+
+
+def test_table_rows_must_match_slot_length():
+    r = _ring()
+    with pytest.raises(ValueError, match="holds 16 tokens but its cos table"):
+        check(24, r, 2, [CachedChunk(0, *_tables(15))], 24)
+    c, s = _tables(16)
+    with pytest.raises(ValueError, match="its sin table"):
+        check(24, r, 2, [CachedChunk(0, c, s[:8])], 24)
+
+
+def test_empty_missing_and_repeated_slots_are_rejected():
+    r = _ring()
+    with pytest.raises(ValueError, match="cached slot 2 is empty"):
+        check(24, r, 1, [CachedChunk(2, *_tables(0))], 24)
+    with pytest.raises(ValueError, match="needs its cos/sin tables"):
+        check(24, r, 2, [CachedChunk(0)], 24)
+    with pytest.raises(ValueError, match="attended twice"):
+        check(24, r, 2, [CachedChunk(0, *_tables(16)), CachedChunk(0, *_tables(16))], 24)
+    with pytest.raises(ValueError, match="not a slot"):
+        check(24, r, 2, [CachedChunk(7, *_tables(16))], 24)
+    r.pre_rope[3] = False
+    with pytest.raises(ValueError, match="holds rotated K; it takes no RoPE tables"):
+        check(24, r, 2, [CachedChunk(3, *_tables(8))], 24)
+
+
+def test_write_bounds():
+    r = _ring()
+    with pytest.raises(ValueError, match="not a slot of the ring"):
+        check(24, r, 4, [], 24)
+    with pytest.raises(ValueError, match="outside"):
+        check(24, r, 1, [], 25)
+    with pytest.raises(ValueError, match="do not fit"):
+        check(40, r, 1, [], 40)
+    with pytest.raises(ValueError, match="need a KV ring"):
+        check(24, None, 1, [], 24)

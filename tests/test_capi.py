@@ -107,18 +107,27 @@ def test_norm_rope_argument_checks(lib):
     _status(lib, lib.joy_fused_qk_norm_rope_3d_paired(p, p, 1, 4, 2, 128, 1e-6, None, p, p, p, None, None),
             1, "non-null")
     f = lib.joy_fused_qkv_norm_rope_cache
-    _status(lib, f(p, 3 * 256, 4, 2, 128, 1e-6, p, p, p, p, p, 256, None, 0, None, 0, p, None, 4, 16, 0, 0,
-                   None), 1, "provided together")
-    _status(lib, f(p, 3 * 256, 4, 2, 128, 1e-6, p, p, p, p, p, 256, None, 0, None, 0, p, p, 4, 16, 4, 0, None),
-            1, "slot 4 out of range")
-    _status(lib, f(p, 3 * 256, 4, 2, 128, 1e-6, p, p, p, p, p, 256, None, 0, None, 0, p, p, 4, 16, 1, 13, None),
-            1, "do not fit")
-    _status(lib, f(p, 100, 4, 2, 128, 1e-6, p, p, p, p, p, 256, None, 0, None, 0, None, None, 0, 0, 0, 0, None),
-            1, "row stride")
-    _status(lib, f(p, 3 * 256, 4, 2, 128, 1e-6, p, p, p, p, p, 256, None, 0, p, 128, None, None, 0, 0, 0, 0,
-                   None), 1, "q_out/k_out/v_out token stride")
-    _status(lib, f(p, 3 * 256, 4, 2, 128, 1e-6, p, p, p, p, p, 256, None, 0, ctypes.c_void_p(0x1008), 256,
-                   None, None, 0, 0, 0, 0, None), 2, "16-byte aligned")
+
+    def call(qkv_stride=3 * 256, q=p, q_st=256, v=None, v_st=0, ck=p, cv=p, slots=4, cap=16, slot=0, off=0,
+             ntok=4, post=0):
+        return f(p, qkv_stride, 4, 2, 128, 1e-6, p, p, p, p, q, q_st, None, 0, v, v_st, ck, cv, slots, cap, slot,
+                 off, ntok, post, None)
+
+    _status(lib, call(cv=None), 1, "provided together")
+    _status(lib, call(slot=4), 1, "slot 4 out of range")
+    _status(lib, call(slot=1, off=13), 1, "do not fit")
+    _status(lib, call(ntok=5), 1, "cache_tokens 5 out of range")
+    _status(lib, call(ntok=-1), 1, "cache_tokens -1 out of range")
+    _status(lib, call(qkv_stride=100, ck=None, cv=None), 1, "row stride")
+    _status(lib, call(v=p, v_st=128, ck=None, cv=None), 1, "q_out/k_out/v_out token stride")
+    _status(lib, call(v=ctypes.c_void_p(0x1008), v_st=256, ck=None, cv=None), 2, "16-byte aligned")
+    _status(lib, call(q=ctypes.c_void_p(0x1008), ck=None, cv=None), 2, "16-byte aligned")
+    # only the first cache_tokens tokens must fit the slot (kv_cache_write_seq_len, dit.py:449-451)
+    _status(lib, call(q=ctypes.c_void_p(0x1008), slot=1, off=14, ntok=2), 2, "16-byte aligned")
+    _status(lib, call(q=ctypes.c_void_p(0x1008), slot=1, off=14, ntok=3), 1, "do not fit")
+    # nothing to write is a successful no-op, even with a null qkv
+    assert f(None, 3 * 256, 4, 2, 128, 1e-6, None, None, None, None, None, 0, None, 0, None, 0, None, None, 0, 0,
+             0, 0, 0, 0, None) == 0
 
 
 def test_single_hip_runtime_in_process():

@@ -110,3 +110,165 @@ def test_block_chain_matches_cpu_reference(n_cached, rounding):
         assert torch.equal(ring.k[c.slot].cpu(), cached_cpu[cached.index(c)][0])
     for slot in range(1, 4 - n_cached):
         assert not ring.k[slot].any() and not ring.v[slot].any()
+
+
+def _chunk_tables(frame, hh, ww, dims=(44, 42, 42), theta=10000.0):
+    """fp32 full-width tables of one cached chunk at temporal position ``frame``."""
+    c32, s32, _, _ = orope.rope_half_tables([frame], hh, ww, dims, theta)
+    return (torch.from_numpy(np.repeat(c32, 2, axis=1)).contiguous(),
+            torch.from_numpy(np.repeat(s32, 2, axis=1)).contiguous())
+
+
+def _half_tables(frames, hh, ww, dims=(44, 42, 42), theta=10000.0):
+    _, _, cb, sb = orope.rope_half_tables(frames, hh, ww, dims, theta)
+    return (torch.from_numpy(cb.view(np.int16)).view(torch.bfloat16),
+            torch.from_numpy(sb.view(np.int16)).view(torch.bfloat16))
+
+
+def test_block_chain_full_size_cfg4():
+    """BASELINE cfg 4 at its workload: video 10800 tokens (3 x 45 x 80) + condition 512, hidden 5120,
+    40 x 128 heads, FFN 13824, 2 cached chunks of 10800 tokens in ring slots 2 and 3, the current
+    chunk written to slot 0. The GPU chain (persistent 256x256 GEMMs with the GELU and gated-residual
+    epilogues, the attention grid over 32912 keys) is held to the CPU oracle on 32 sampled rows per
+    stream: every K / V row is computed on the CPU, attention and the row-local tail for the sampled
+    rows; the ring slot is checked on every token."""
+    from joyomni_ops.dit_block import CachedChunk, KVRing, QuantizedDoubleStreamBlock
+    announce("block chain full size cfg4")
+    E, H, FFN, T = 5120, 40, 13824, 512
+    D = E // H
+    frames, hh, ww = 3, 45, 80
+    L = frames * hh * ww
+    g = gen(404)
+    blk = QuantizedDoubleStreamBlock(E, H, FFN, DEV, g)
+    img = torch.randn(1, L, E, generator=g).to(torch.bfloat16)
+    txt = torch.randn(1, T, E, generator=g).to(torch.bfloat16)
+    vec = torch.randn(1, E, generator=g).to(torch.bfloat16)
+    cos_h, sin_h = _half_tables([6, 7, 8], hh, ww)      # current chunk after two cached chunks of 3 frames
+    ring = KVRing(4, L, H, D, DEV)
+    cached, cached_cpu = [], []
+    for i, slot in enumerate((2, 3)):
+        kpre = torch.randn(L, H, D, generator=g).to(torch.bfloat16)
+        val = torch.randn(L, H, D, generator=g).to(torch.bfloat16)
+        ring.k[slot].copy_(kpre)
+        ring.v[slot].copy_(val)
+        ring.lengths[slot] = L
+        c32, s32, _, _ = orope.rope_half_tables([3 * i, 3 * i + 1, 3 * i + 2], hh, ww, (44, 42, 42), 10000.0)
+        cf = torch.from_numpy(np.repeat(c32, 2, axis=1)).contiguous()
+        sf = torch.from_numpy(np.repeat(s32, 2, axis=1)).contiguous()
+        cached.append(CachedChunk(slot, cf.to(DEV), sf.to(DEV)))
+        cached_cpu.append((kpre, val, cf, sf))
+    out_img, out_txt = blk.forward(img.to(DEV), txt.to(DEV), vec.to(DEV), cos_h.to(DEV), sin_h.to(DEV),
+                                   ring=ring, write_slot=0, cached=cached)
+    torch.cuda.synchronize()
+    ri = torch.from_numpy(np.sort(np.random.default_rng(3).choice(L, 32, replace=False)))
+    rt = torch.from_numpy(np.sort(np.random.default_rng(4).choice(T, 32, replace=False)))
+    ri[-1], rt[-1] = L - 1, T - 1
+    sd = (stream_dict(blk.img), stream_dict(blk.txt))
+    del blk
+    r_img, r_txt, r_kpre, r_v = torch_path.double_stream_block(
+        img[0], txt[0], vec, sd, H, cos_h, sin_h, cached_cpu, out_rows=(ri, rt))
+    pert = img[0].clone().view(torch.int16)
+    pert[torch.rand(pert.shape, generator=gen(8)) < 0.01] ^= 1
+    p_img, p_txt, _, _ = torch_path.double_stream_block(
+        pert.view(torch.bfloat16), txt[0], vec, sd, H, cos_h, sin_h, cached_cpu, out_rows=(ri, rt))
+    e_img = rms_rel(out_img[0, ri.to(DEV)].cpu(), r_img, img[0, ri])
+    e_txt = rms_rel(out_txt[0, rt.to(DEV)].cpu(), r_txt, txt[0, rt])
+    s_img = rms_rel(p_img, r_img, img[0, ri])
+    s_txt = rms_rel(p_txt, r_txt, txt[0, rt])
+    f_k, e_k = ulp_frac(ring.k[0].cpu(), r_kpre)
+    f_v, e_v = ulp_frac(ring.v[0].cpu(), r_v)
+    print(f"cfg4 block errors (RMS of update, sampled rows): img {e_img:.3e} txt {e_txt:.3e}; reference "
+          f"1-ulp sensitivity img {s_img:.3e} txt {s_txt:.3e}; ring k_pre {f_k:.2e} beyond 1 ulp, RMS {e_k:.3e};"
+          f" v {f_v:.2e}, {e_v:.3e}")
+    assert e_img <= 3e-2 and e_txt <= 3e-2, (e_img, e_txt)
+    assert e_img <= 1.5 * s_img + 1e-3 and e_txt <= 1.5 * s_txt + 1e-3, (e_img, s_img, e_txt, s_txt)
+    assert f_k <= 1e-3 and f_v <= 1e-3 and e_k <= 1e-2 and e_v <= 1e-2, (f_k, e_k, f_v, e_v)
+    for i, (slot, cc) in enumerate(zip((2, 3), cached_cpu)):
+        assert torch.equal(ring.k[slot].cpu(), cc[0]) and torch.equal(ring.v[slot].cpu(), cc[1])
+    assert not ring.k[1].any() and not ring.v[1].any()
+
+
+def _small_block(seed, E=512, H=4, FFN=1536, hh=12, ww=20, T=32):
+    from joyomni_ops.dit_block import QuantizedDoubleStreamBlock
+    g = gen(seed)
+    blk = QuantizedDoubleStreamBlock(E, H, FFN, DEV, g)
+    L = hh * ww
+    img = torch.randn(1, L, E, generator=g).to(torch.bfloat16)
+    txt = torch.randn(1, T, E, generator=g).to(torch.bfloat16)
+    vec = torch.randn(1, E, generator=g).to(torch.bfloat16)
+    return g, blk, img, txt, vec
+
+
+@pytest.mark.parametrize("pre_rope", [True, False])
+def test_block_cache_only_forward(pre_rope):
+    """kv_cache_write_only (dit.py:446-459): img / txt come back unchanged; the first
+    kv_cache_write_seq_len tokens' K (before RoPE or rotated) and V reach the ring slot."""
+    from joyomni_ops.dit_block import KVRing
+    announce("block cache-only forward", pre_rope)
+    g, blk, img, txt, vec = _small_block(50 + pre_rope)
+    L, H, D, n = img.shape[1], 4, 128, 150
+    cos_h, sin_h = _half_tables([1], 12, 20)
+    ring = KVRing(3, L, H, D, DEV)
+    img_d, txt_d = img.to(DEV), txt.to(DEV)
+    oi, ot = blk.forward(img_d, txt_d, vec.to(DEV), cos_h.to(DEV), sin_h.to(DEV), ring=ring, write_slot=1,
+                         kv_cache_write_only=True, kv_cache_write_seq_len=n, kv_cache_pre_rope=pre_rope)
+    torch.cuda.synchronize()
+    assert oi is img_d and ot is txt_d and torch.equal(img_d.cpu(), img)
+    assert ring.lengths == [0, n, 0] and ring.pre_rope[1] == pre_rope
+    sd = (stream_dict(blk.img), stream_dict(blk.txt))
+    _, _, rk, rv = torch_path.double_stream_block(img[0], txt[0], vec, sd, H, cos_h, sin_h, write_only=True,
+                                                  cache_tokens=n, cache_pre_rope=pre_rope, division_min_k=8192)
+    f_k, e_k = ulp_frac(ring.k[1, :n].cpu(), rk)
+    f_v, e_v = ulp_frac(ring.v[1, :n].cpu(), rv)
+    assert f_k <= 1e-3 and f_v <= 1e-3 and e_k <= 1e-2 and e_v <= 1e-2, (f_k, e_k, f_v, e_v)
+    assert not ring.k[1, n:].any() and not ring.k[0].any() and not ring.k[2].any()
+
+
+@pytest.mark.parametrize("mixed", [False, True])
+def test_block_image_only_forward(mixed):
+    """skip_text_stream (dit.py:481-487,500-506): attention over [cached | video], txt unchanged;
+    one cached slot holds K before RoPE (rotated on read), and with ``mixed`` a second one holds K
+    stored rotated (copied as is, dit.py:258-271); the current chunk's first 200 tokens go to the ring."""
+    from joyomni_ops.dit_block import CachedChunk, KVRing
+    announce("block image-only forward", mixed)
+    g, blk, img, txt, vec = _small_block(60 + mixed)
+    L, H, D, n = img.shape[1], 4, 128, 200
+    cos_h, sin_h = _half_tables([2], 12, 20)
+    ring = KVRing(4, L, H, D, DEV)
+    cached, cached_cpu = [], []
+    kpre = torch.randn(L, H, D, generator=g).to(torch.bfloat16)
+    val = torch.randn(L, H, D, generator=g).to(torch.bfloat16)
+    ring.k[3].copy_(kpre)
+    ring.v[3].copy_(val)
+    ring.lengths[3] = L
+    cf, sf = _chunk_tables(0, 12, 20)
+    cached.append(CachedChunk(3, cf.to(DEV), sf.to(DEV)))
+    cached_cpu.append((kpre, val, cf, sf))
+    if mixed:
+        krot = torch.randn(100, H, D, generator=g).to(torch.bfloat16)
+        v2 = torch.randn(100, H, D, generator=g).to(torch.bfloat16)
+        ring.k[2, :100].copy_(krot)
+        ring.v[2, :100].copy_(v2)
+        ring.lengths[2], ring.pre_rope[2] = 100, False
+        cached.append(CachedChunk(2))
+        cached_cpu.append((krot, v2, None, None))
+    txt_d = txt.to(DEV)
+    oi, ot = blk.forward(img.to(DEV), txt_d, vec.to(DEV), cos_h.to(DEV), sin_h.to(DEV), ring=ring, write_slot=0,
+                         cached=cached, skip_text_stream=True, kv_cache_write_seq_len=n)
+    torch.cuda.synchronize()
+    assert ot is txt_d and torch.equal(txt_d.cpu(), txt)
+    sd = (stream_dict(blk.img), stream_dict(blk.txt))
+    r_img, _, rk, rv = torch_path.double_stream_block(img[0], txt[0], vec, sd, H, cos_h, sin_h, cached_cpu,
+                                                      skip_text_stream=True, cache_tokens=n)
+    pert = img[0].clone().view(torch.int16)
+    pert[torch.rand(pert.shape, generator=gen(9)) < 0.01] ^= 1
+    p_img, _, _, _ = torch_path.double_stream_block(pert.view(torch.bfloat16), txt[0], vec, sd, H, cos_h, sin_h,
+                                                    cached_cpu, skip_text_stream=True, cache_tokens=n)
+    e_img = rms_rel(oi[0].cpu(), r_img, img[0])
+    s_img = rms_rel(p_img, r_img, img[0])
+    print(f"image-only block: img {e_img:.3e} (reference 1-ulp sensitivity {s_img:.3e})")
+    assert e_img <= 3e-2 and e_img <= 1.5 * s_img + 1e-3, (e_img, s_img)
+    f_k, e_k = ulp_frac(ring.k[0, :n].cpu(), rk)
+    f_v, e_v = ulp_frac(ring.v[0, :n].cpu(), rv)
+    assert f_k <= 1e-3 and e_k <= 1e-2 and f_v <= 1e-3 and e_v <= 1e-2, (f_k, e_k, f_v, e_v)
+    assert not ring.k[0, n:].any() and ring.lengths[0] == n

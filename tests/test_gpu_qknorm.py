@@ -133,3 +133,108 @@ def test_fused_without_cache_or_k_out():
     torch.cuda.synchronize()
     oq_, _, _, _ = oqk.qkv_norm_rope_cache(u16(qkv), H, 1e-6, u16(qw), u16(kw), u16(cos), u16(sin))
     assert_close(u16(q_out), oq_, "q")
+
+
+def test_short_or_foreign_outputs_raise_before_launch():
+    """An output view with fewer (or more) tokens than qkv rows is rejected before anything runs;
+    the canary buffers stay untouched."""
+    announce("fused qkv short outputs")
+    import joyomni_ops as jo
+    L, H, D = 24, 2, 128
+    qkv, qw, kw, cos, sin = cfg1_inputs(L, H, D, 1, 4, 6, (44, 42, 42), 10000.0, 7)
+    args = (qkv.to(DEV), H, 1e-6, qw.to(DEV), kw.to(DEV), cos.to(DEV), sin.to(DEV))
+    full = torch.zeros(L, H, D, dtype=torch.bfloat16, device=DEV)
+    canary = torch.zeros(1, L, H, D, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError, match="holds 23 tokens, expected 24"):
+        jo.fused_qkv_norm_rope_cache(*args, canary[0, :L - 1], None, None, None, 0, 0)
+    with pytest.raises(RuntimeError, match="k_out holds 23 tokens"):
+        jo.fused_qkv_norm_rope_cache(*args, full, canary[:, 1:], None, None, 0, 0)
+    with pytest.raises(RuntimeError, match="v_out holds 25 tokens"):
+        big = torch.zeros(L + 1, H * D, dtype=torch.bfloat16, device=DEV)
+        jo.fused_qkv_norm_rope_cache(*args, full, None, None, None, 0, 0, v_out=big)
+    with pytest.raises(RuntimeError, match="on the device of qkv"):
+        jo.fused_qkv_norm_rope_cache(*args, torch.zeros(L, H, D, dtype=torch.bfloat16), None, None, None, 0, 0)
+    torch.cuda.synchronize()
+    assert not canary.any() and not full.any()
+
+
+@pytest.mark.parametrize("pre_rope", [True, False])
+def test_fused_qkv_partial_cache_write(pre_rope):
+    """kv_cache_write_seq_len (dit.py:449-451): only the first n tokens reach the ring; the ring
+    keeps K before RoPE or rotated (kv_cache_pre_rope, dit.py:432-433); Q/K/V outputs cover all L."""
+    announce("fused qkv partial cache", pre_rope)
+    import joyomni_ops as jo
+    L, H, D, n = 96, 4, 128, 61
+    qkv, qw, kw, cos, sin = cfg1_inputs(L, H, D, 2, 6, 8, (44, 42, 42), 10000.0, 8)
+    q_out = torch.empty(L, H, D, dtype=torch.bfloat16, device=DEV)
+    k_out = torch.empty_like(q_out)
+    v_out = torch.empty_like(q_out)
+    ck = torch.zeros(3, 70, H, D, dtype=torch.bfloat16, device=DEV)
+    cv = torch.zeros_like(ck)
+    jo.fused_qkv_norm_rope_cache(qkv.to(DEV), H, 1e-6, qw.to(DEV), kw.to(DEV), cos.to(DEV), sin.to(DEV),
+                                 q_out, k_out, ck, cv, 2, 9, v_out=v_out, cache_tokens=n, cache_pre_rope=pre_rope)
+    torch.cuda.synchronize()
+    oq_, ok_, okp, ov = oqk.qkv_norm_rope_cache(u16(qkv), H, 1e-6, u16(qw), u16(kw), u16(cos), u16(sin))
+    assert_close(u16(q_out), oq_, "q")
+    assert_close(u16(k_out), ok_, "k")
+    assert np.array_equal(u16(v_out), ov)
+    assert_close(u16(ck[2, 9:9 + n]), (okp if pre_rope else ok_)[:n], "ring k")
+    assert np.array_equal(u16(cv[2, 9:9 + n]), ov[:n])
+    if not pre_rope:  # the rotated ring K is the attention K itself
+        assert torch.equal(ck[2, 9:9 + n], k_out[:n])
+    assert not ck[2, :9].any() and not ck[2, 9 + n:].any() and not cv[2, 9 + n:].any()
+    assert not ck[:2].any() and not cv[:2].any()
+
+
+def test_fused_qkv_cache_only_forward():
+    """kv_cache_write_only (dit.py:446-459): no Q/K/V outputs, only the ring; Q is not read."""
+    announce("fused qkv cache only")
+    import joyomni_ops as jo
+    L, H, D = 50, 4, 128
+    qkv, qw, kw, cos, sin = cfg1_inputs(L, H, D, 1, 5, 10, (44, 42, 42), 10000.0, 9)
+    qkv_d = qkv.to(DEV)
+    qkv_d[:, : H * D] = float("nan")  # Q is not read: NaNs there cannot reach the ring
+    ck = torch.zeros(2, L, H, D, dtype=torch.bfloat16, device=DEV)
+    cv = torch.zeros_like(ck)
+    jo.fused_qkv_norm_rope_cache(qkv_d, H, 1e-6, qw.to(DEV), kw.to(DEV), cos.to(DEV), sin.to(DEV),
+                                 None, None, ck, cv, 1, 0)
+    torch.cuda.synchronize()
+    _, _, okp, ov = oqk.qkv_norm_rope_cache(u16(qkv), H, 1e-6, u16(qw), u16(kw), u16(cos), u16(sin))
+    assert_close(u16(ck[1]), okp, "ring k")
+    assert np.array_equal(u16(cv[1]), ov) and not ck[0].any()
+
+
+def test_fused_qkv_on_source_id_tables_at_production_geometry():
+    """Composed [current | ref-video] tables (dit.py:1093-1155, config.py:29-37) at the reference's
+    480x832 chunk: 2 x 30 x 52 tokens per segment, 32 heads, RoPE 16/56/56 theta 256, role theta 256
+    over 128 dims; the first 3120 tokens (the current chunk) go to the ring."""
+    from joyomni_ops import rope
+    announce("fused qkv source-id tables")
+    import joyomni_ops as jo
+    frames, hh, ww, H, D = 2, 30, 52, 32, 128
+    n_cur = frames * hh * ww
+    L = 2 * n_cur
+    g = gen(10)
+    qkv = bf(torch.randn(L, 3 * H * D, generator=g))
+    qw = bf(1 + 0.1 * torch.randn(D, generator=g))
+    kw = bf(1 + 0.1 * torch.randn(D, generator=g))
+    cos, sin = rope.visual_rope_half_tables((frames, hh, ww), frames)
+    _, _, cb, sb = orope.visual_half_tables((frames, hh, ww), frames)
+    assert np.all(np.abs(u16(cos).astype(np.int32) - cb.astype(np.int32)) <= 1)
+    q_out = torch.empty(L, H, D, dtype=torch.bfloat16, device=DEV)
+    k_out = torch.empty_like(q_out)
+    ck = torch.zeros(2, n_cur, H, D, dtype=torch.bfloat16, device=DEV)
+    cv = torch.zeros_like(ck)
+    jo.fused_qkv_norm_rope_cache(qkv.to(DEV), H, 1e-6, qw.to(DEV), kw.to(DEV), cos.to(DEV), sin.to(DEV),
+                                 q_out, k_out, ck, cv, 0, 0, cache_tokens=n_cur)
+    torch.cuda.synchronize()
+    toks = np.sort(np.random.default_rng(1).choice(L, 384, replace=False))
+    toks[0], toks[-1] = 0, L - 1
+    ti = torch.from_numpy(toks)
+    oq_, ok_, okp, _ = oqk.qkv_norm_rope_cache(u16(qkv[ti]), H, 1e-6, u16(qw), u16(kw), cb[toks], sb[toks])
+    tid = ti.to(DEV)
+    assert_close(u16(q_out[tid]), oq_, "q")
+    assert_close(u16(k_out[tid]), ok_, "k")
+    cur = toks < n_cur
+    assert_close(u16(ck[0][tid[torch.from_numpy(cur)]]), okp[cur], "ring k (current chunk)")
+    assert torch.equal(cv[0].reshape(n_cur, -1), qkv.to(DEV)[:n_cur, 2 * H * D:])

@@ -74,3 +74,28 @@ def test_rope_tables_match_oracle():
     # which can move a bf16 rounding by one step.
     assert np.mean(c == cb) > 0.99 and np.mean(s == sb) > 0.99
     assert np.all(np.abs(c.astype(np.int32) - cb.astype(np.int32)) <= 1)
+
+
+def test_visual_rope_tables_match_oracle():
+    """The product's [current | ref-video] tables (dit.py:1093-1166) equal the oracle's bf16 bits
+    (up to one step where torch's fp32 cos/sin round differently), at the production dims."""
+    import numpy as np
+    from oracle import rope as orope
+    for kw in ({}, {"ref_image_cache": True}, {"temporal_ids": torch.tensor([3, 4])}):
+        cos, sin = rope.visual_rope_half_tables((2, 4, 6), 2, **kw)
+        okw = dict(kw)
+        if "temporal_ids" in okw:
+            okw["temporal_ids"] = okw["temporal_ids"].numpy()
+        _, _, cb, sb = orope.visual_half_tables((2, 4, 6), 2, **okw)
+        c = cos.view(torch.int16).numpy().view(np.uint16)
+        s = sin.view(torch.int16).numpy().view(np.uint16)
+        assert cos.shape == (2 * 2 * 4 * 6, 64)
+        assert np.mean(c == cb) > 0.99 and np.mean(s == sb) > 0.99
+        assert np.all(np.abs(c.astype(np.int32) - cb.astype(np.int32)) <= 1)
+        assert np.all(np.abs(s.astype(np.int32) - sb.astype(np.int32)) <= 1)
+    # target tokens alone: the plain 3-D tables
+    c0, s0 = rope.visual_rope_half_tables((2, 4, 6), None)
+    c1, s1 = rope.rope_3d_half_tables(2, 4, 6, (16, 56, 56), 256.0)
+    assert torch.equal(c0, c1) and torch.equal(s0, s1)
+    with pytest.raises(ValueError, match="temporal ids"):
+        rope.visual_rope_tables((2, 4, 6), 3, temporal_ids=torch.tensor([0, 1]))
