@@ -184,11 +184,25 @@ def test_cfg2_ffn_up_gelu_full_m_sampled_rows():
     ref32 = og.gelu_tanh(og.reference_fp32(qa_s, qw_u8, sa_s, sw, u16(bias)))
     rms = float(np.sqrt(np.mean(ref32.astype(np.float64) ** 2)))
     assert np.abs(ys - ref32).max() <= 2e-2 * rms
-    plain_bits, _ = og.scaled_mm(qa_s, qw_u8, sa_s, sw, u16(bias))
-    exp = bf16_to_f32(f32_to_bf16(og.gelu_tanh(bf16_to_f32(plain_bits)))).astype(np.float64)
-    step = np.spacing(np.abs(exp).astype(np.float32)).astype(np.float64) * 65536.0
-    far = np.abs(ys - exp) > step + 1e-6
-    assert np.count_nonzero(far) <= 1e-3 * far.size, np.count_nonzero(far)
+    # GELU of the pre-GELU value: the kernel's rounded GEMM output is within one bf16 step plus the
+    # fp32 accumulation allowance of the oracle's exactly accumulated one (as the plain epilogue is
+    # checked); GELU maps that interval to [lo, hi] (its one minimum at x = -0.7518 included), and
+    # the result is one more bf16 rounding away. Where |gelu| << |x| (x < -1) one input step is
+    # several output steps, so the envelope, not a fixed ulp count, is the bound.
+    plain_bits, o = og.scaled_mm(qa_s, qw_u8, sa_s, sw, u16(bias))
+    x = bf16_to_f32(plain_bits).astype(np.float64)
+    S = og.abs_acc(qa_s, qw_u8) * sa_s.astype(np.float64)[:, None] * sw.astype(np.float64)[None, :]
+    u = np.spacing(np.abs(x).astype(np.float32)).astype(np.float64) * 65536.0 + 2.0 ** -14 * S
+    ga, gb = og.gelu_tanh(x - u).astype(np.float64), og.gelu_tanh(x + u).astype(np.float64)
+    lo, hi = np.minimum(ga, gb), np.maximum(ga, gb)
+    xm = -0.7517916
+    lo = np.where((x - u <= xm) & (xm <= x + u), np.minimum(lo, float(og.gelu_tanh(np.array([xm]))[0])), lo)
+    step = lambda v: np.spacing(np.abs(v).astype(np.float32)).astype(np.float64) * 65536.0  # noqa: E731
+    bad = (ys < lo - step(lo) - 1e-7) | (ys > hi + step(hi) + 1e-7)
+    assert not bad.any(), (np.count_nonzero(bad), ys[bad][:4], lo[bad][:4], hi[bad][:4])
+    # most outputs equal GELU of the oracle's own rounded value exactly
+    exp = bf16_to_f32(f32_to_bf16(og.gelu_tanh(x))).astype(np.float64)
+    assert np.mean(ys == exp) > 0.95
     assert np.abs(ys - bf16_to_f32(plain_bits)).max() > 1e-2  # the epilogue did apply GELU
 
 
