@@ -105,6 +105,28 @@ JOY_API joy_status joy_fp8_scaled_mm(const void *mat_a, const void *mat_b, const
 JOY_API int64_t joy_fp8_scaled_mm_workspace_size(int64_t M, int64_t N, int64_t K);
 
 /*
+ * Bytes of the library-owned split-K scratch that joy_fp8_scaled_mm_noalloc uses
+ * (one file-scope device array, held by every GPU the library runs on until the
+ * process ends).
+ */
+#define JOY_FP8_NOALLOC_SCRATCH_BYTES (32LL * 1024 * 1024)
+
+/*
+ * joy_fp8_scaled_mm without a workspace argument: allocates nothing (no hipMalloc, no
+ * hipFree, no allocating library call), for callers that cannot allocate (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid it). No counterpart in
+ * the reference. Same arguments, rules and results as joy_fp8_scaled_mm with a
+ * workspace of joy_fp8_scaled_mm_workspace_size(M, N, K) bytes; the split-K partial
+ * sums go to the library's scratch array of JOY_FP8_NOALLOC_SCRATCH_BYTES instead.
+ * Problems whose split-K plan needs more scratch than that return
+ * JOY_ERR_UNSUPPORTED before anything is launched. Every call on one GPU shares that
+ * GPU's scratch: calls that overlap on one GPU (different streams or threads) race.
+ */
+JOY_API joy_status joy_fp8_scaled_mm_noalloc(const void *mat_a, const void *mat_b, const float *scales_a,
+                                             const float *scales_b, const void *bias, void *out, int out_dtype,
+                                             int64_t M, int64_t N, int64_t K, int epilogue, void *stream);
+
+/*
  * FP8 GEMM with the gated residual of the DiT block fused into its epilogue (new
  * op, no single reference counterpart): the out-projection / FFN-down Fp8Linear
  * (fp8_linear.py:114-141) followed by fused_add_gate = torch.addcmul(residual, y,

@@ -4,6 +4,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "../../include/joyomni_hip.h"
 #include "joy_kernels.hpp"
 
@@ -88,6 +90,32 @@ joy_status scaled_mm_common(const void* mat_a, const void* mat_b, const float* s
 }
 
 
+// Split-K scratch of joy_fp8_scaled_mm_noalloc: one device array per GPU, part of the
+// library's code object. Host code never passes the array's name to a kernel (on the
+// host it is a stand-in, not a device address); it uses the per-device address that
+// hipGetSymbolAddress returns, fetched once per device on that device's first call.
+static __device__ __align__(256) unsigned char scratch[JOY_FP8_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+joy_status scratch_for_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(JOY_ERR_UNSUPPORTED, "device %d: at most %d devices", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_status(e, "hipGetSymbolAddress(scratch)");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return JOY_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -122,6 +150,24 @@ joy_status joy_fp8_scaled_mm(const void* mat_a, const void* mat_b, const float* 
                              int64_t workspace_bytes, void* stream) {
   return scaled_mm_common(mat_a, mat_b, scales_a, scales_b, bias, out, out_dtype, M, N, K, epilogue, nullptr, 0,
                           nullptr, workspace, workspace_bytes, stream);
+}
+
+joy_status joy_fp8_scaled_mm_noalloc(const void* mat_a, const void* mat_b, const float* scales_a,
+                                     const float* scales_b, const void* bias, void* out, int out_dtype, int64_t M,
+                                     int64_t N, int64_t K, int epilogue, void* stream) {
+  const int64_t need = joy_fp8_scaled_mm_workspace_size(M, N, K);
+  if (need > JOY_FP8_NOALLOC_SCRATCH_BYTES)
+    return fail(JOY_ERR_UNSUPPORTED,
+                "fp8_scaled_mm_noalloc: the split-K plan of %lldx%lldx%lld needs %lld bytes of scratch, "
+                "the library holds %lld",
+                (long long)M, (long long)N, (long long)K, (long long)need, (long long)JOY_FP8_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (need > 0) {
+    const joy_status st = scratch_for_current_device(&ws);
+    if (st != JOY_OK) return st;
+  }
+  return scaled_mm_common(mat_a, mat_b, scales_a, scales_b, bias, out, out_dtype, M, N, K, epilogue, nullptr, 0,
+                          nullptr, ws, need, stream);
 }
 
 int64_t joy_fp8_scaled_mm_workspace_size(int64_t M, int64_t N, int64_t K) {

@@ -26,6 +26,8 @@ JOY_NORM_RMS = 1
 JOY_QUANT_DIVIDE = 0
 JOY_QUANT_RECIPROCAL = 1
 
+JOY_FP8_NOALLOC_SCRATCH_BYTES = 32 * 1024 * 1024
+
 JOY_EPILOGUE_NONE = 0
 JOY_EPILOGUE_GELU_TANH = 1
 
@@ -50,6 +52,7 @@ SIGNATURES = {
     "joy_per_token_quant_fp8": (_int, [_vp, _int, _vp, _vp, _i64, _i64, _int, _vp]),
     "joy_fp8_scaled_mm": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _int, _i64, _i64, _i64, _int, _vp, _i64, _vp]),
     "joy_fp8_scaled_mm_workspace_size": (_i64, [_i64, _i64, _i64]),
+    "joy_fp8_scaled_mm_noalloc": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _int, _i64, _i64, _i64, _int, _vp]),
     "joy_fp8_scaled_mm_gated_residual": (
         _int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _int, _i64, _i64, _i64, _vp, _i64, _vp]),
     "joy_fused_qk_norm_rope_3d_paired": (

@@ -1,0 +1,80 @@
+"""GPU: the allocation-free FP8 GEMM entry point (joy_fp8_scaled_mm_noalloc) against the
+workspace entry point (joy_fp8_scaled_mm), through the C ABI. Both run the same kernels and the
+same split-K plan, so the outputs must be bit-identical: calls in a row (the second on a
+smaller problem, so stale partial sums of the first would show), a problem that needs no
+scratch, and the largest split plan of the device, which fills the whole scratch."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import DEV, announce, gen, outlier_acts, u16
+from oracle import quant as oq
+
+pytestmark = pytest.mark.gpu
+
+
+def _problem(M, N, K, seed):
+    g = gen(seed)
+    x = outlier_acts(M, K, g)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    bias = (torch.randn(N, generator=g) * 0.01).to(torch.bfloat16)
+    qa, sa = oq.quant_per_token(u16(x), "bf16", "div")
+    qw, sw = oq.quant_weight_per_channel(u16(w))
+    dev8 = lambda q: torch.from_numpy(np.ascontiguousarray(q)).view(torch.float8_e4m3fn).to(DEV)  # noqa: E731
+    return (dev8(qa), dev8(qw), torch.from_numpy(sa).to(DEV), torch.from_numpy(sw).to(DEV), bias.to(DEV))
+
+
+def _call(lib, fn, a, w, sa, sw, bias, out, M, N, K, epilogue, *ws):
+    stream = torch.cuda.current_stream().cuda_stream
+    return getattr(lib, fn)(a.data_ptr(), w.data_ptr(), sa.data_ptr(), sw.data_ptr(), bias.data_ptr(),
+                            out.data_ptr(), 0, M, N, K, epilogue, *ws, stream)
+
+
+def _both(lib, M, N, K, epilogue, seed):
+    from joyomni_ops import _lib
+    a, w, sa, sw, bias = _problem(M, N, K, seed)
+    need = lib.joy_fp8_scaled_mm_workspace_size(M, N, K)
+    ws = torch.empty(max(need, 16), dtype=torch.uint8, device=DEV)
+    ref = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=DEV)
+    got = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=DEV)
+    _lib.check(lib, _call(lib, "joy_fp8_scaled_mm", a, w, sa, sw, bias, ref, M, N, K, epilogue,
+                          ws.data_ptr(), need))
+    _lib.check(lib, _call(lib, "joy_fp8_scaled_mm_noalloc", a, w, sa, sw, bias, got, M, N, K, epilogue))
+    torch.cuda.synchronize()
+    return need, ref, got
+
+
+def test_noalloc_matches_workspace_entry_point():
+    import joyomni_ops as jo
+    lib = jo._LIB
+    cases = [(256, 5120, 5120, 0), (64, 5120, 5120, 1), (96, 2048, 4096, 0), (1024, 512, 512, 0)]
+    splits_seen = 0
+    for i, (M, N, K, epi) in enumerate(cases):
+        announce("noalloc gemm", M, N, K, epi)
+        need, ref, got = _both(lib, M, N, K, epi, 100 + i)
+        assert need <= jo._lib.JOY_FP8_NOALLOC_SCRATCH_BYTES
+        splits_seen += need > 0
+        assert not torch.isnan(ref.float()).any()
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), (M, N, K)
+    assert splits_seen >= 3  # the first three problems take split-K plans (the scratch is used)
+
+
+def test_noalloc_uses_the_whole_scratch_and_every_plan_fits():
+    """A split plan needs at most (CUs / tiles) * tiles * 128 x 256 x 4 bytes = CUs * 128 KiB, the
+    32 MiB of the scratch on a 256-CU MI355X: 512 x 4096 x 8192 needs all of it and still matches
+    the workspace entry point bit for bit; no small-M shape of the sweep needs more."""
+    import joyomni_ops as jo
+    from joyomni_ops import _lib
+    lib = jo._LIB
+    cap = _lib.JOY_FP8_NOALLOC_SCRATCH_BYTES
+    worst = max(lib.joy_fp8_scaled_mm_workspace_size(m, n, k) for m in range(16, 513, 16)
+                for n in (512, 1024, 2048, 3072, 4096, 5120, 8192, 13824, 15360) for k in (4096, 5120, 8192, 13824))
+    assert 0 < worst <= cap, worst
+    M, N, K = 512, 4096, 8192
+    announce("noalloc gemm full scratch", M, N, K)
+    need, ref, got = _both(lib, M, N, K, 0, 200)
+    assert need == worst == cap, (need, worst, cap)
+    assert not torch.isnan(ref.float()).any()
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
