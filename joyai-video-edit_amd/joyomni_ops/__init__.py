@@ -747,25 +747,29 @@ def _fake_fused_text_qkv_pack(txt_q, txt_k, txt_v, txt_q_weight, txt_k_weight, e
 # --------------------------------------------------------------------------
 def fused_qk_norm_rope_3d_paired(q, k, seq_len, num_heads, eps, q_weight, k_weight, cos, sin,
                                  k_pre_rope=None):
-    """In-place fused RMSNorm(q,k) + 3D RoPE. q/k: [B, seq_len*num_heads, head_dim] bf16."""
+    """Per-head RMSNorm then interleaved RoPE on q and k, written over them (bf16 [B, seq_len * num_heads,
+    head_dim]); ``k_pre_rope`` optionally receives k after the norm and before the rotation."""
     _ops.fused_qk_norm_rope_3d_paired(q, k, seq_len, num_heads, eps, q_weight, k_weight, cos, sin,
                                       k_pre_rope)
 
 
 def fused_joint_qkv_pack(img_q, img_k, img_v, txt_q, txt_k, txt_v, cached_k, cached_v,
                          txt_q_weight, txt_k_weight, eps=1e-6):
-    """Pack joint-attention Q/K/V and fuse text Q/K RMSNorm (bf16, B=1, D=128)."""
+    """Joint attention operands in fresh tensors: Q = [image | normed text], K / V = [cache | image | text],
+    the text q / k RMS-normalised with two roundings; batch 1, head_dim 128, bf16."""
     return _ops.fused_joint_qkv_pack(img_q, img_k, img_v, txt_q, txt_k, txt_v, cached_k, cached_v,
                                      txt_q_weight, txt_k_weight, eps)
 
 
 def fused_cached_kv_pack(key0, value0, key1, value1, cos, sin):
-    """Rotate and pack one or two pre-RoPE cache segments (bf16, B=1, D=128)."""
+    """Cached keys stored before RoPE (one or two segments) rotated with fp32 full-width tables and
+    concatenated, values concatenated alongside; batch 1, head_dim 128, bf16."""
     return _ops.fused_cached_kv_pack(key0, value0, key1, value1, cos, sin)
 
 
 def fused_norm_scale_shift(x, gamma, beta, scale, shift, norm_type, eps=1e-5):
-    """Norm(x; gamma, beta) * (1 + scale) + shift. norm_type: 'layer' or 'rms'."""
+    """LayerNorm or RMSNorm of each row of x (optional affine gamma / beta), then adaLN modulation
+    ``* (1 + scale) + shift``; ``norm_type`` is ``"layer"`` or ``"rms"``."""
     nt = 0 if norm_type == "layer" else 1 if norm_type == "rms" else -1
     return _ops.fused_norm_scale_shift(x, gamma, beta, scale, shift, nt, eps)
 
@@ -781,7 +785,7 @@ def fused_norm_scale_shift_fp8(x, gamma, beta, scale, shift, norm_type, eps, out
 
 
 def rmsnorm(x, weight, eps=1e-6):
-    """(x / RMS(x)) * weight. x: [M, N], weight: [N]."""
+    """Row-wise RMS normalisation of x [M, N] scaled by weight [N]."""
     return _ops.rmsnorm(x, weight, eps)
 
 

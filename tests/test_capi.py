@@ -18,11 +18,16 @@ def declared_functions():
     return sorted(set(re.findall(r"JOY_API\s+[\w\s\*]+?\b(joy_\w+)\s*\(", text)))
 
 
+# JOY_HIP_LIB names another build of the library to check (the sanitizer build of
+# tests/test_sanitized_capi.py); by default the in-tree library.
+LIB_PATH = os.environ.get("JOY_HIP_LIB", _lib.LIB_PATH)
+
+
 @pytest.fixture(scope="module")
 def lib():
-    if not os.path.exists(_lib.LIB_PATH):
-        pytest.fail(f"{_lib.LIB_PATH} missing: run __graft_entry__.build()")
-    return _lib.load()
+    if not os.path.exists(LIB_PATH):
+        pytest.fail(f"{LIB_PATH} missing: run __graft_entry__.build()")
+    return _lib.load(LIB_PATH)
 
 
 def test_header_declares_expected_entry_points():
@@ -31,7 +36,7 @@ def test_header_declares_expected_entry_points():
 
 
 def test_library_exports_every_declared_symbol(lib):
-    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True,
+    out = subprocess.run(["nm", "-D", "--defined-only", LIB_PATH], capture_output=True, text=True,
                          check=True).stdout
     exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
     for name in declared_functions():
