@@ -10,6 +10,7 @@ launch stream, plus the reference's CPU torch path timed on the host cores on a
 bounded sample (``cpu_baseline``).
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu] [--only qkv|gemm|...]
+       [--tunableop results.csv]
 """
 from __future__ import annotations
 
@@ -211,6 +212,76 @@ def bench_gemm(steps, warmup):
              for r in res if r.get("reference_hipblaslt_tflops")]
     ref_agg = tot_flops / sum(ref_t) / 1e12 if len(ref_t) == len(res) else None
     return res, tot_flops / tot_t / 1e12, ref_agg
+
+
+def bench_cfg0(steps, warmup):
+    """BASELINE cfg 0: one Fp8Linear forward (per-token activation quant + FP8 GEMM + bias) at
+    256 x 4096 -> 4096, the shape the CPU baseline times; W streams from HBM (rotated copies)."""
+    import torch
+    import joyomni_ops as jo
+    from joyomni_ops.fp8_linear import Fp8Linear
+    dev = torch.device("cuda:0")
+    M, K, N = 256, 4096, 4096
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(M, K, generator=g)
+    x[:, torch.randperm(K, generator=g)[: K // 200]] *= 20
+    x = x.to(torch.bfloat16).to(dev)
+    lin = torch.nn.Linear(K, N)
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn(N, K, generator=g) * 0.02)
+        lin.bias.copy_(torch.randn(N, generator=g) * 0.01)
+    layers = [Fp8Linear.from_linear(lin.to(torch.bfloat16).to(dev))]
+    layers += [Fp8Linear(layers[0].weight_fp8.clone(), layers[0].weight_scale, layers[0].bias)
+               for _ in range(buffer_sets(N * K) - 1)]
+    t = time_launches(Rotation(layers, lambda f: f(x)), steps, warmup)
+    qx, sx = jo_quant(x)
+    t_mm = time_launches(Rotation(layers, lambda f: jo.fp8_scaled_mm(
+        qx, f.weight_fp8, sx, f.weight_scale, torch.bfloat16, f.bias)), steps, warmup)
+    return {"workload": f"cfg0 Fp8Linear forward {M}x{K} -> {N} (act quant + GEMM + bias)", "us": t * 1e6,
+            "tflops": 2 * M * N * K / t / 1e12, "gbs": gemm_bytes(M, N, K) / t / 1e9,
+            "weight_copies": len(layers), "gemm_only_us": t_mm * 1e6}
+
+
+def jo_quant(x):
+    import torch
+    import joyomni_ops as jo
+    q = torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=x.device)
+    s = torch.empty(x.shape[0], 1, device=x.device)
+    jo.sgl_per_token_quant_fp8(x, q, s)
+    return q, s
+
+
+def bench_clock(steps, warmup):
+    """The QKV GEMM (cfg 2) launched back to back on the bench's random operands, then on all-zero
+    operands, then on the random ones again; each launch timed with HIP events on the stream. Under
+    rocprofv3 --pmc SQ_BUSY_CYCLES the per-dispatch busy cycles over these durations give the shader
+    clock per operand kind (the part is power-limited; switching activity sets the clock)."""
+    import torch
+    import joyomni_ops as jo
+    dev = torch.device("cuda:0")
+    M, K, N = L_TOK, 5120, 15360
+    g = torch.Generator().manual_seed(K + N)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    bias = (torch.randn(N, generator=g) * 0.01).to(torch.bfloat16).to(dev)
+    qa, sa = jo_quant(x)
+    qw, sw = jo_quant(w)
+    za, zw = torch.zeros_like(qa), torch.zeros_like(qw)
+    stream = torch.cuda.current_stream()
+    out = {}
+    for name, a, b in (("random", qa, qw), ("zeros", za, zw), ("random_again", qa, qw)):
+        for _ in range(warmup):
+            jo.fp8_scaled_mm(a, b.t(), sa, sw.reshape(1, N), torch.bfloat16, bias)
+        ts = []
+        for _ in range(steps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            jo.fp8_scaled_mm(a, b.t(), sa, sw.reshape(1, N), torch.bfloat16, bias)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1e3)
+        out[name] = {"us": ts, "median_us": sorted(ts)[len(ts) // 2]}
+    return {"workload": f"QKV GEMM {M}x{K}x{N}, bf16 out + bias", "launches": out}
 
 
 # The reference's own production GEMM shapes (M, K, N), tuned for gfx950 by
@@ -513,20 +584,24 @@ def cpu_baseline_gemm():
     from oracle import torch_path
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    Ms, K, N = 256, 5120, 15360
-    g = torch.Generator().manual_seed(1)
-    x = torch.randn(Ms, K, generator=g).to(torch.bfloat16)
+    Ms, K, N = 256, 4096, 4096  # BASELINE cfg 0
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(Ms, K, generator=g)
+    x[:, torch.randperm(K, generator=g)[: K // 200]] *= 20
+    x = x.to(torch.bfloat16)
     wq, ws = torch_path.quantize_per_token((torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16))
-    bias = torch.zeros(N, dtype=torch.bfloat16)
+    bias = (torch.randn(N, generator=g) * 0.01).to(torch.bfloat16)
     torch_path.fp8_linear(x, wq, ws, bias)
     times = []
-    for _ in range(3):
+    for _ in range(5):
         t0 = time.perf_counter()
         torch_path.fp8_linear(x, wq, ws, bias)
         times.append(time.perf_counter() - t0)
-    t = sorted(times)[1]
+    t = sorted(times)[2]
     return {"value": 2 * Ms * N * K / t / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
-            "sample": f"QKV shape, {Ms} of {L_TOK} rows, median of 3, quant + fp32 dequant-matmul"}
+            "us": t * 1e6,
+            "sample": f"cfg0 single FP8 linear {Ms}x{K} -> {N}, median of 5: per-token quant (division) + "
+                      "fp32 dequantise-then-matmul + bias -> bf16"}
 
 
 def main():
@@ -537,7 +612,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time plain launches (no HIP graph)")
     ap.add_argument("--only", default="all",
-                    choices=["all", "qkv", "gemm", "refgemm", "small", "quant", "pack", "norm", "attn", "block", "copy"])
+                    choices=["all", "qkv", "gemm", "cfg0", "refgemm", "small", "quant", "pack", "norm", "attn", "block",
+                             "copy", "clock"])
+    ap.add_argument("--tunableop", metavar="CSV", default=None,
+                    help="tune the reference's torch._scaled_mm legs with PyTorch TunableOp first, with the "
+                         "reference's settings (deploy/tune_rocm_fp8.py: 10 ms, 30 iterations), results to CSV")
     args = ap.parse_args()
     global EAGER
     EAGER = args.eager
@@ -548,6 +627,14 @@ def main():
 
     import torch
     import joyomni_ops  # noqa: F401  (fails loudly if the HIP library is missing)
+    if args.tunableop:
+        from torch.cuda import tunable
+        tunable.set_filename(args.tunableop, insert_device_ordinal=False)
+        tunable.enable(True)
+        tunable.tuning_enable(True)
+        tunable.record_untuned_enable(False)
+        tunable.set_max_tuning_duration(10)
+        tunable.set_max_tuning_iterations(30)
     props = torch.cuda.get_device_properties(0)
     rec = {"metric": METRIC, "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
@@ -580,6 +667,9 @@ def main():
         progress(f"cfg2 GEMMs {agg:.0f} TFLOP/s aggregate")
         if "value" not in rec:
             rec.update({"value": round(agg, 1), "unit": "TFLOP/s", "ms_per_step": sum(r["ms"] for r in res)})
+    if args.only in ("all", "cfg0"):
+        rec["cfg0_linear"] = bench_cfg0(args.steps, args.warmup)
+        progress(f"cfg0 linear {rec['cfg0_linear']['us']:.1f} us")
     if args.only in ("all", "refgemm"):
         rs = bench_reference_shapes(args.steps, max(2, args.warmup // 2))
         t_ours = sum(r["us"] for r in rs)
@@ -608,10 +698,15 @@ def main():
         progress(f"cfg4 block {rec['block_cfg4']['block_latency_ms']:.2f} ms")
     if args.only == "copy":
         rec["copy"] = bench_copy(args.steps, args.warmup)
+    if args.only == "clock":
+        rec["clock"] = bench_clock(max(args.steps, 13), max(args.warmup, 1))
+    if args.tunableop:
+        from torch.cuda import tunable
+        rec["tunableop"] = {"file": args.tunableop, "tuned_results": len(tunable.get_results())}
     if not args.no_cpu:
         if args.only in ("all", "qkv"):
             rec["cpu_baseline"] = cpu_baseline_qkv()
-        if args.only in ("all", "gemm"):
+        if args.only in ("all", "gemm", "cfg0"):
             rec["cpu_baseline_gemm"] = cpu_baseline_gemm()
     print(json.dumps(rec), flush=True)
 

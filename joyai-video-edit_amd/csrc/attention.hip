@@ -22,7 +22,8 @@
 //     addresses apply the same permutation. The O^T accumulator again gives each lane one
 //     query, so the rescale by exp2(m_old - m_new) is per lane.
 // The two halves are software-pipelined inside the wave: S(0); S(1) with the softmax of half 0
-// on the VALU; PV(0) with the softmax of half 1; PV(1).
+// on the VALU; PV(0) with the softmax of half 1; PV(1). The A operands of the tile's 32 MFMAs
+// (K, then the transposed V) are fetched from LDS two MFMAs ahead of their use.
 // K and V tiles reach LDS by buffer DMA straight into LDS (double-buffered, the next tile in
 // flight during the current one, one barrier per tile); LDS rows of 256 bytes store 16-byte
 // chunk c at a row-dependent XOR of c (chunk_at, chunk_at_v).
@@ -235,56 +236,47 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_d128(AttnArgs a) {
     v16f s0, s1;
     v4i p0[2], p1[2];
     Soft st0, st1;
-    // S(0)
-    {
-      v4i kf[2];
-      kf[0] = k_operand(kt, 0, 0);
+    // The tile's 32 MFMAs read one stream of A operands -- K of half 0, K of half 1, V of half 0,
+    // V of half 1 -- each fetched from LDS kOperandAhead MFMAs before it is used (one register set
+    // per fetch in flight; with the 2 waves per SIMD this hides most of the LDS latency, and at
+    // two fetches ahead the kernel still fits 256 registers without spilling).
+    constexpr int kOperandAhead = 2;
+    constexpr int NB = kOperandAhead + 1;
+    v4i ob[NB];
+    auto operand = [&](int i) -> v4i {
+      if (i < 8) return k_operand(kt, 0, i);
+      if (i < 16) return k_operand(kt, 1, i - 8);
+      if (i < 24) return pv_operand(vt, 0, i - 16);
+      return pv_operand(vt, 1, i - 24);
+    };
 #pragma unroll
-      for (int st = 0; st < 8; ++st) {
-        if (st + 1 < 8) kf[(st + 1) & 1] = k_operand(kt, 0, st + 1);
-        s0 = mfma_bf16(as_bf16x8(kf[st & 1]), as_bf16x8(qf[st]), st == 0 ? (v16f){} : s0);
+    for (int i = 0; i < NB - 1; ++i) ob[i] = operand(i);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      if (i + NB - 1 < 32) ob[(i + NB - 1) % NB] = operand(i + NB - 1);
+      const v4i op = ob[i % NB];
+      if (i < 8) {  // S(0)
+        s0 = mfma_bf16(as_bf16x8(op), as_bf16x8(qf[i]), i == 0 ? (v16f){} : s0);
+      } else if (i < 16) {  // S(1) with softmax(0)
+        s1 = mfma_bf16(as_bf16x8(op), as_bf16x8(qf[i - 8]), i == 8 ? (v16f){} : s1);
+        soft_step(i - 8, s0, p0, st0);
+      } else if (i < 24) {  // PV(0) with softmax(1)
+        o[(i - 16) & 3] = mfma_bf16(as_bf16x8(op), as_bf16x8(p0[(i - 16) >> 2]), o[(i - 16) & 3]);
+        soft_step(i - 16, s1, p1, st1);
+      } else {  // PV(1)
+        o[(i - 24) & 3] = mfma_bf16(as_bf16x8(op), as_bf16x8(p1[(i - 24) >> 2]), o[(i - 24) & 3]);
       }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    if constexpr (partial) mask(s0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    // S(1) with softmax(0)
-    {
-      v4i kf[2];
-      kf[0] = k_operand(kt, 1, 0);
-#pragma unroll
-      for (int st = 0; st < 8; ++st) {
-        if (st + 1 < 8) kf[(st + 1) & 1] = k_operand(kt, 1, st + 1);
-        s1 = mfma_bf16(as_bf16x8(kf[st & 1]), as_bf16x8(qf[st]), st == 0 ? (v16f){} : s1);
-        soft_step(st, s0, p0, st0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (i == 7) {
+        if constexpr (partial) mask(s0, 0);
         __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-    rescale(st0.alpha);
-    if constexpr (partial) mask(s1, 1);
-    __builtin_amdgcn_sched_barrier(0);
-    // PV(0) with softmax(1)
-    {
-      v4i va[2];
-      va[0] = pv_operand(vt, 0, 0);
-#pragma unroll
-      for (int n = 0; n < 8; ++n) {
-        if (n + 1 < 8) va[(n + 1) & 1] = pv_operand(vt, 0, n + 1);
-        o[n & 3] = mfma_bf16(as_bf16x8(va[n & 1]), as_bf16x8(p0[n >> 2]), o[n & 3]);
-        soft_step(n, s1, p1, st1);
+      } else if (i == 15) {
+        rescale(st0.alpha);
+        if constexpr (partial) mask(s1, 1);
         __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-    rescale(st1.alpha);
-    __builtin_amdgcn_sched_barrier(0);
-    // PV(1)
-    {
-      v4i va[2];
-      va[0] = pv_operand(vt, 1, 0);
-#pragma unroll
-      for (int n = 0; n < 8; ++n) {
-        if (n + 1 < 8) va[(n + 1) & 1] = pv_operand(vt, 1, n + 1);
-        o[n & 3] = mfma_bf16(as_bf16x8(va[n & 1]), as_bf16x8(p1[n >> 2]), o[n & 3]);
+      } else if (i == 23) {
+        rescale(st1.alpha);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
     __builtin_amdgcn_sched_barrier(0);
