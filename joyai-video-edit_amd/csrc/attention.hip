@@ -9,9 +9,9 @@
 // in elements), so the joint operands are read where the fused QKV / pack ops wrote
 // them and O is written straight into the [L, H*128] rows the out-projection reads.
 //
-// One workgroup = 128 queries of one head (4 waves x 32 queries, two workgroups per CU), one
-// pass over the keys in tiles of 64 (flash attention with an online softmax), each tile as two
-// 32-key halves with a softmax step each. Per half and wave:
+// One wave = 32 queries of one head, 8 waves per workgroup (one workgroup per CU), one pass over
+// the keys in tiles of 64 (flash attention with an online softmax), each tile as two 32-key
+// halves with a softmax step each. Per half and wave:
 //   * S^T = K Q^T: 8 v_mfma_f32_32x32x16_bf16 (K from LDS as the A operand, the wave's 32
 //     queries kept in registers as the B operand). In the 32x32 output a lane holds 16 keys of
 //     ONE query, so the row max / row sum are in-lane plus one exchange with lane ^ 32;
@@ -98,18 +98,38 @@ __device__ __forceinline__ float xor32_sum(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// One query block per wave (4 waves, two workgroups per CU), each 64-key tile processed as two
-// 32-key halves with an online-softmax step each, so that within the wave the VALU work of one
-// half overlaps the MFMAs of the other: S(0); S(1) with softmax(0); PV(0) with softmax(1);
-// PV(1). A softmax step follows each MFMA in program order (sched_barrier keeps it there).
-__global__ __launch_bounds__(256, 2) void attn_fwd_d128(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2][2][kTileB];  // [buffer][K, V]
+// One query block of 32 queries per wave, 8 waves per workgroup (one workgroup per CU, two waves
+// per SIMD): the workgroup's 256 queries share every K / V tile it moves into LDS, half the DMA
+// traffic per query of 128-query workgroups (measured 3.5 % faster at the cfg-4 shape). Each
+// 64-key tile is processed as two 32-key halves with an online-softmax step each, so that within
+// the wave the VALU work of one half overlaps the MFMAs of the other: S(0); S(1) with
+// softmax(0); PV(0) with softmax(1); PV(1). A softmax step follows each MFMA in program order
+// (sched_barrier keeps it there).
+//
+// Work split: the query blocks of all heads form one list (head-major, qb_per_head blocks per
+// head) and workgroup w takes blocks 8 w .. 8 w + 7, so the grid has ceil(heads * qb_per_head / 8)
+// workgroups whatever the query count per head (per-head workgroups would leave a nearly empty
+// last round at 11312 queries: 45 x 40 = 1800 = 7.03 rounds of 256 CUs). A workgroup whose blocks
+// straddle a head boundary moves the K / V tiles of both heads (LDS holds two heads' tiles);
+// qb_per_head >= 8 keeps it to two heads. Blocks past the list (last workgroup) compute on the
+// last valid block and store nothing.
+constexpr int kWaves = 8;
+__global__ __launch_bounds__(64 * kWaves, 1) void attn_fwd_d128(AttnArgs a, int qb_per_head) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2][2][2][kTileB];  // [buffer][head slot][K, V]
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int head = blockIdx.y;
   const int ql = lane & 31, hf = lane >> 5;
   const int64_t Lq = a.q_len, Lk = a.k_len;
-  const int qrow = blockIdx.x * 128 + wave * 32 + ql;
+  const int nblocks = a.heads * qb_per_head;
+  const int blk0 = (int)blockIdx.x * kWaves;
+  const int head_lo = blk0 / qb_per_head;
+  const int head_hi = (min(blk0 + kWaves, nblocks) - 1) / qb_per_head;  // blk0 < nblocks
+  const bool straddle = head_hi != head_lo;
+  const int blk = min(blk0 + wave, nblocks - 1);
+  const bool active = blk0 + wave < nblocks;
+  const int head = blk / qb_per_head;
+  const int hslot = head == head_lo ? 0 : 1;
+  const int qrow = (blk - head * qb_per_head) * 32 + ql;
 
   v4i qf[8];
   {
@@ -119,27 +139,32 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_d128(AttnArgs a) {
     for (int st = 0; st < 8; ++st) qf[st] = *(const v4i*)(qp + 16 * st);
   }
 
-  // K / V tiles by buffer DMA: wave w moves rows 16 w .. 16 w + 15 of each, 4 DMAs of 4 rows.
+  // K / V tiles by buffer DMA: wave w moves rows 8 w .. 8 w + 7 of each (two DMAs of 4 rows), for
+  // the workgroup's first head and, when it straddles a head boundary, its second head.
   // The buffer descriptors are rebuilt per tile, based at the tile's first key and ending after
   // its last key below Lk: rows past Lk load zeros (their scores are -inf), and the offsets stay
   // below 64 rows whatever the sequence length.
-  const uint16_t* kbase = a.k.ptr + (int64_t)head * a.k.stride_head;
-  const uint16_t* vbase = a.v.ptr + (int64_t)head * a.v.stride_head;
   const int64_t ks = a.k.stride_token, vs = a.v.stride_token;
-  auto dma_tile = [&](int buf, int64_t k0) {
+  auto dma_head = [&](int buf, int slot, int h, int64_t k0) {
+    const uint16_t* kb = a.k.ptr + (int64_t)h * a.k.stride_head;
+    const uint16_t* vb = a.v.ptr + (int64_t)h * a.v.stride_head;
     const int rows = (int)min((int64_t)kBK, Lk - k0);
     const __amdgpu_buffer_rsrc_t krs =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(kbase + k0 * ks), 0, (int)(((rows - 1) * ks + kD) * 2), 0x00020000);
+        __builtin_amdgcn_make_buffer_rsrc((void*)(kb + k0 * ks), 0, (int)(((rows - 1) * ks + kD) * 2), 0x00020000);
     const __amdgpu_buffer_rsrc_t vrs =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(vbase + k0 * vs), 0, (int)(((rows - 1) * vs + kD) * 2), 0x00020000);
+        __builtin_amdgcn_make_buffer_rsrc((void*)(vb + k0 * vs), 0, (int)(((rows - 1) * vs + kD) * 2), 0x00020000);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = wave * 16 + i * 4 + (lane >> 4);
+    for (int i = 0; i < 2; ++i) {
+      const int row = wave * 8 + i * 4 + (lane >> 4);
       dma16_buf(krs, (uint32_t)(row * ks * 2 + ((lane & 15) ^ (row & 15)) * 16), 0,
-                (lds_void*)&lds[buf][0][(wave * 16 + i * 4) * kRowB]);
+                (lds_void*)&lds[buf][slot][0][(wave * 8 + i * 4) * kRowB]);
       dma16_buf(vrs, (uint32_t)(row * vs * 2 + ((lane & 15) ^ vsw(row)) * 16), 0,
-                (lds_void*)&lds[buf][1][(wave * 16 + i * 4) * kRowB]);
+                (lds_void*)&lds[buf][slot][1][(wave * 8 + i * 4) * kRowB]);
     }
+  };
+  auto dma_tile = [&](int buf, int64_t k0) {
+    dma_head(buf, 0, head_lo, k0);
+    if (straddle) dma_head(buf, 1, head_hi, k0);
   };
 
   const int tg = lane >> 4, ta = lane & 15;
@@ -223,8 +248,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_d128(AttnArgs a) {
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     if (t + 1 < ntiles) dma_tile(buf ^ 1, (t + 1) * kBK);
-    const uint8_t* kt = lds[buf][0];
-    const uint8_t* vt = lds[buf][1];
+    const uint8_t* kt = lds[buf][hslot][0];
+    const uint8_t* vt = lds[buf][hslot][1];
     const int64_t k0 = t * kBK;
     auto mask = [&](v16f& s, int kb) {
 #pragma unroll
@@ -296,7 +321,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_d128(AttnArgs a) {
   }
   __builtin_amdgcn_s_waitcnt(0x0070);
 
-  if (qrow < Lq) {
+  if (active && qrow < Lq) {
     const float inv = 1.0f / l_run;
     uint16_t* op = a.out + (int64_t)qrow * a.out_stride_token + (int64_t)head * kD;
 #pragma unroll
@@ -316,12 +341,17 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_d128(AttnArgs a) {
 
 // Tried and dropped (same inputs, cfg-4 joint shape): two query blocks per wave, pipelined inside
 // the wave at one wave per SIMD (bit-identical outputs, 9.8 vs 8.2 ms: the scores no longer fit
-// the architectural registers and every tile pays accumulator-register copies), and the same
-// kernel without the half-tile split (MFMA busy 49 % at 1.94 GHz against 54 % at 1.83 GHz here:
-// the part is power-limited, so the better overlap buys 2.6 %).
+// the architectural registers and every tile pays accumulator-register copies; rebuilt with two
+// waves per workgroup it spills to scratch), and the same kernel without the half-tile split
+// (MFMA busy 49 % at 1.94 GHz against 54 % at 1.83 GHz here: the part is power-limited, so the
+// better overlap buys 2.6 %). A three-stage K / V ring (next-but-one tile in flight) measured no
+// faster than two stages.
 hipError_t launch_attention_fwd(const AttnArgs& a, hipStream_t st) {
-  const dim3 grid((unsigned)((a.q_len + 127) / 128), (unsigned)a.heads);
-  hipLaunchKernelGGL(attn_fwd_d128, grid, dim3(256), 0, st, a);
+  // query blocks per head: at least kWaves, so a workgroup spans at most two heads
+  const int qb = (int)max((a.q_len + 31) / 32, (int64_t)kWaves);
+  const int64_t blocks = (int64_t)a.heads * qb;
+  const dim3 grid((unsigned)((blocks + kWaves - 1) / kWaves));
+  hipLaunchKernelGGL(attn_fwd_d128, grid, dim3(64 * kWaves), 0, st, a, qb);
   return hipGetLastError();
 }
 

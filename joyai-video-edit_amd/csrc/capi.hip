@@ -543,7 +543,8 @@ joy_status joy_attention_fwd(const joy_bf16_view* q, const joy_bf16_view* k, con
   }
   if (!aligned(out, 16) || out_stride_token % 8 != 0)
     return fail(JOY_ERR_UNSUPPORTED, "out needs 16-byte aligned rows");
-  if ((q->len + 127) / 128 > 0x7fffffffLL) return fail(JOY_ERR_UNSUPPORTED, "sequence too long");
+  if (num_heads * ((q->len + 31) / 32 + 8) > 0x7fffffffLL)
+    return fail(JOY_ERR_UNSUPPORTED, "num_heads * query blocks of 32 above 2^31");
   joy::AttnArgs a;
   a.q = row_view(q);
   a.k = row_view(k);

@@ -50,6 +50,17 @@ def test_random_shapes(Lq, Lk, H):
     _check(_run(q, k, v), q, k, v, f"{Lq}x{Lk}x{H}")
 
 
+@pytest.mark.parametrize("Lq,H", [(330, 7), (256, 3), (225, 2), (40, 9)])
+def test_workgroups_straddling_heads(Lq, H):
+    """Workgroups take 8 consecutive 32-query blocks of the head-major block list, so one
+    workgroup can hold the end of one head and the start of the next (330 queries: 11 blocks per
+    head), or padding blocks past Lq (40 queries: 2 of 8 blocks); every row of every head is
+    checked."""
+    announce("attention straddling heads", Lq, H)
+    q, k, v = _inputs(Lq, 300, H, Lq + 17 * H)
+    _check(_run(q, k, v), q, k, v, f"{Lq}x300x{H}")
+
+
 def test_peaked_scores_and_explicit_scale():
     """Large-magnitude q/k (peaked softmax, exp2 range) and a non-default scale."""
     announce("attention peaked")
