@@ -160,17 +160,22 @@ __device__ __forceinline__ void store_tile_lds(const v16f (&acc)[FN][FM], const 
         *(uint2*)(srow + (i * 32 + q * 8 + g * 4) * 2) = pk;
       }
   }
-  // read back: CPL lanes per row, 64/CPL rows per instruction
+  // read back: CPL lanes per row, 64/CPL rows per instruction (FN = 3: 12 lanes per row,
+  // 5 rows per instruction, lanes 60..63 idle and the last instruction's rows past the
+  // tile skipped)
   constexpr int CPL = ROW_BYTES / 16;
   constexpr int RPI = 64 / CPL;
+  constexpr int ROWS = 32 * FM;
   const int rr = lane / CPL, cc = lane % CPL;
   const int n = n_base + cc * 8;
   uint4 gv = make_uint4(0, 0, 0, 0);
   if constexpr (kEpi == kEpiResidual)
     if (n < N) gv = *(const uint4*)(res.gate + n);
 #pragma unroll
-  for (int r0 = 0; r0 < 32 * FM; r0 += RPI) {
+  for (int r0 = 0; r0 < ROWS; r0 += RPI) {
     const int r = r0 + rr;
+    if constexpr (RPI * CPL != 64 || ROWS % RPI != 0)
+      if (rr >= RPI || r >= ROWS) continue;
     uint4 v = *(const uint4*)(stage + r * PITCH + cc * 16);
     const int m = m_base + r;
     if (m < M && n < N) {
@@ -1315,13 +1320,18 @@ hipError_t launch_gemm_t(const GemmArgs& g, hipStream_t st) {
     // 140.3 us vs 151.7. At K 4096 only where the 128-row tiles fit one round:
     // 1024 x 4096 x 4096 26.9 us vs 30.1, 1560 x 4096 x 4096 42.6 vs 44.2, while
     // 1024 x 4096 x 12288 (1.5 rounds of 128x256) takes 82.5 us vs 66.6.
+    // Where neither 128-row tile fits one round but 256x192 tiles do (1024 x 4096 x 12288:
+    // 256 tiles against 192 of 256x256), the 256x192 tiles fill every CU.
     const int P = device_cus();
     const int64_t t256 = (int64_t)((g.M + 255) / 256) * ((g.N + 255) / 256);
     const int64_t t128 = (int64_t)((g.M + 127) / 128) * ((g.N + 127) / 128);
     const int64_t t128x256 = (int64_t)((g.M + 127) / 128) * ((g.N + 255) / 256);
+    const int64_t t256x192 = (int64_t)((g.M + 255) / 256) * ((g.N + 191) / 192);
     if (t256 < P) {
       if (t128 <= P) return launch_deepk<kBf16, kEpi, 128, 128, 128, 3, 3>(g, 1, nullptr, st);
-      if (g.K >= 8192 || t128x256 <= P) return launch_deepk<kBf16, kEpi, 128, 256, 128, 2, 3>(g, 1, nullptr, st);
+      if (t128x256 <= P) return launch_deepk<kBf16, kEpi, 128, 256, 128, 2, 3>(g, 1, nullptr, st);
+      if (t256x192 <= P) return launch_direct<kBf16, kEpi, 256, 192, 5>(g, st);
+      if (g.K >= 8192) return launch_deepk<kBf16, kEpi, 128, 256, 128, 2, 3>(g, 1, nullptr, st);
     }
   }
   if (fast) return launch_4w<kBf16, kEpi>(g, st);

@@ -65,7 +65,10 @@ def assert_acc_bound(y_bits, qa, qw, sa, sw, bias, what):
                                    (513, 520, 384), (64, 1024, 4096),
                                    # small-M (skinny) kernel: one row, fewer 128-byte K chunks
                                    # than waves, uneven chunks per wave, partial column tiles
-                                   (1, 520, 384), (65, 72, 1280), (200, 4104, 640), (256, 15360, 128)])
+                                   (1, 520, 384), (65, 72, 1280), (200, 4104, 640), (256, 15360, 128),
+                                   # 256x192 tiles (less than one round of them, 128-row tiles
+                                   # more than one): partial last row and column tiles
+                                   (600, 13832, 4096)])
 def test_exact_small_integers_bit_exact(M, N, K):
     """fp8 integers in [-8, 8] and power-of-two scales: every partial sum is exact,
     so the output is fixed to the last bit whatever the summation order."""
@@ -83,7 +86,8 @@ def test_exact_small_integers_bit_exact(M, N, K):
     assert np.array_equal(u16(gemm(qa, qw, sa, sw, None)), exp_nb)
 
 
-@pytest.mark.parametrize("M,N,K", [(300, 264, 256), (64, 520, 384), (33, 40, 48), (520, 4104, 128)])
+@pytest.mark.parametrize("M,N,K", [(300, 264, 256), (64, 520, 384), (33, 40, 48), (520, 4104, 128),
+                                   (600, 13832, 4096)])
 def test_fp16_output_with_denormal_bias(M, N, K):
     """fp16 output, a quarter of the fp16 bias values denormal (k * 2^-24): the zero
     activation rows output the bias itself, so a flushed denormal shows; exact small
