@@ -150,3 +150,18 @@ def test_cfg4_joint_shape_sampled_queries():
     err_ours = _check(out, q, k, v, "cfg4 ours", rows=rows)
     err_sdpa = _check(ref_sdpa, q, k, v, "cfg4 torch sdpa", rows=rows)
     print(f"cfg4 max|err| vs float64: ours {err_ours:.3e}, torch SDPA {err_sdpa:.3e}")
+
+
+@pytest.mark.parametrize("Lk", [3467, 11267])
+def test_reference_production_shape_sampled_queries(Lk):
+    """The reference's own production attention (480x832 chunk: 3467 queries over 3467..11267
+    keys, 32 heads of 128): 48 sampled queries against the oracle. 3467 = 108 blocks of 32 + 11
+    rows: a partial last query block, 108 blocks per head (workgroups straddle heads), and a
+    partial last key tile (11267 = 176 tiles of 64 + 3 keys)."""
+    announce("attention reference production", 3467, Lk, 32)
+    Lq, H = 3467, 32
+    q, k, v = _inputs(Lq, Lk, H, 77 + Lk)
+    out = _run(q, k, v)
+    rows = np.sort(np.random.default_rng(Lk).choice(Lq, 48, replace=False))
+    rows[0], rows[-1] = 0, Lq - 1
+    _check(out, q, k, v, f"production {Lq}x{Lk}x{H}", rows=rows)

@@ -125,36 +125,27 @@ def _half_tables(frames, hh, ww, dims=(44, 42, 42), theta=10000.0):
             torch.from_numpy(sb.view(np.int16)).view(torch.bfloat16))
 
 
-def test_block_chain_full_size_cfg4():
-    """BASELINE cfg 4 at its workload: video 10800 tokens (3 x 45 x 80) + condition 512, hidden 5120,
-    40 x 128 heads, FFN 13824, 2 cached chunks of 10800 tokens in ring slots 2 and 3, the current
-    chunk written to slot 0. The GPU chain (persistent 256x256 GEMMs with the GELU and gated-residual
-    epilogues, the attention grid over 32912 keys) is held to the CPU oracle on 32 sampled rows per
-    stream: every K / V row is computed on the CPU, attention and the row-local tail for the sampled
-    rows; the ring slot is checked on every token."""
+def _full_block_check(E, H, FFN, T, cos_h, sin_h, cached_tables, seed):
+    """One block at full size: the GPU chain held to the CPU oracle on 32 sampled rows per stream
+    (every K / V row is computed on the CPU, attention and the row-local tail for the sampled rows);
+    the ring slot written by the chunk is checked on every token, the cached slots stay unchanged."""
     from joyomni_ops.dit_block import CachedChunk, KVRing, QuantizedDoubleStreamBlock
-    announce("block chain full size cfg4")
-    E, H, FFN, T = 5120, 40, 13824, 512
     D = E // H
-    frames, hh, ww = 3, 45, 80
-    L = frames * hh * ww
-    g = gen(404)
+    L = cos_h.shape[0]
+    g = gen(seed)
     blk = QuantizedDoubleStreamBlock(E, H, FFN, DEV, g)
     img = torch.randn(1, L, E, generator=g).to(torch.bfloat16)
     txt = torch.randn(1, T, E, generator=g).to(torch.bfloat16)
     vec = torch.randn(1, E, generator=g).to(torch.bfloat16)
-    cos_h, sin_h = _half_tables([6, 7, 8], hh, ww)      # current chunk after two cached chunks of 3 frames
+    slots = (2, 3)[:len(cached_tables)]
     ring = KVRing(4, L, H, D, DEV)
     cached, cached_cpu = [], []
-    for i, slot in enumerate((2, 3)):
+    for slot, (cf, sf) in zip(slots, cached_tables):
         kpre = torch.randn(L, H, D, generator=g).to(torch.bfloat16)
         val = torch.randn(L, H, D, generator=g).to(torch.bfloat16)
         ring.k[slot].copy_(kpre)
         ring.v[slot].copy_(val)
         ring.lengths[slot] = L
-        c32, s32, _, _ = orope.rope_half_tables([3 * i, 3 * i + 1, 3 * i + 2], hh, ww, (44, 42, 42), 10000.0)
-        cf = torch.from_numpy(np.repeat(c32, 2, axis=1)).contiguous()
-        sf = torch.from_numpy(np.repeat(s32, 2, axis=1)).contiguous()
         cached.append(CachedChunk(slot, cf.to(DEV), sf.to(DEV)))
         cached_cpu.append((kpre, val, cf, sf))
     out_img, out_txt = blk.forward(img.to(DEV), txt.to(DEV), vec.to(DEV), cos_h.to(DEV), sin_h.to(DEV),
@@ -177,15 +168,47 @@ def test_block_chain_full_size_cfg4():
     s_txt = rms_rel(p_txt, r_txt, txt[0, rt])
     f_k, e_k = ulp_frac(ring.k[0].cpu(), r_kpre)
     f_v, e_v = ulp_frac(ring.v[0].cpu(), r_v)
-    print(f"cfg4 block errors (RMS of update, sampled rows): img {e_img:.3e} txt {e_txt:.3e}; reference "
-          f"1-ulp sensitivity img {s_img:.3e} txt {s_txt:.3e}; ring k_pre {f_k:.2e} beyond 1 ulp, RMS {e_k:.3e};"
-          f" v {f_v:.2e}, {e_v:.3e}")
+    print(f"block {E}/{H}x{D}/{FFN}, {L}+{T} tokens: errors (RMS of update, sampled rows): img {e_img:.3e} "
+          f"txt {e_txt:.3e}; reference 1-ulp sensitivity img {s_img:.3e} txt {s_txt:.3e}; ring k_pre "
+          f"{f_k:.2e} beyond 1 ulp, RMS {e_k:.3e}; v {f_v:.2e}, {e_v:.3e}")
     assert e_img <= 3e-2 and e_txt <= 3e-2, (e_img, e_txt)
     assert e_img <= 1.5 * s_img + 1e-3 and e_txt <= 1.5 * s_txt + 1e-3, (e_img, s_img, e_txt, s_txt)
     assert f_k <= 1e-3 and f_v <= 1e-3 and e_k <= 1e-2 and e_v <= 1e-2, (f_k, e_k, f_v, e_v)
-    for i, (slot, cc) in enumerate(zip((2, 3), cached_cpu)):
+    for slot, cc in zip(slots, cached_cpu):
         assert torch.equal(ring.k[slot].cpu(), cc[0]) and torch.equal(ring.v[slot].cpu(), cc[1])
     assert not ring.k[1].any() and not ring.v[1].any()
+
+
+def _full_tables(frames, hh, ww):
+    c32, s32, _, _ = orope.rope_half_tables(frames, hh, ww, (44, 42, 42), 10000.0)
+    return (torch.from_numpy(np.repeat(c32, 2, axis=1)).contiguous(),
+            torch.from_numpy(np.repeat(s32, 2, axis=1)).contiguous())
+
+
+def test_block_chain_full_size_cfg4():
+    """BASELINE cfg 4 at its workload: video 10800 tokens (3 x 45 x 80) + condition 512, hidden 5120,
+    40 x 128 heads, FFN 13824, 2 cached chunks of 10800 tokens in ring slots 2 and 3, the current
+    chunk written to slot 0: persistent 256x256 GEMMs with the GELU and gated-residual epilogues,
+    the attention grid over 32912 keys."""
+    announce("block chain full size cfg4")
+    hh, ww = 45, 80
+    cos_h, sin_h = _half_tables([6, 7, 8], hh, ww)      # current chunk after two cached chunks of 3 frames
+    cached = [_full_tables([3 * i, 3 * i + 1, 3 * i + 2], hh, ww) for i in range(2)]
+    _full_block_check(5120, 40, 13824, 512, cos_h, sin_h, cached, 404)
+
+
+def test_block_chain_reference_production_geometry():
+    """The reference's production block at 480x832: hidden 4096, 32 x 128 heads, FFN 16384; the
+    visual sequence is one latent frame of the current chunk plus one reference-video frame
+    (2 x 30 x 52 = 3120 tokens, RoPE 16/56/56 theta 256 composed with the source-id rotation of the
+    reference frame), 512 condition tokens and one cached chunk. M = 3120 and 512 take the
+    one-round / split-tail and small-M GEMM plans; attention is 3632 queries over 6752 keys."""
+    from joyomni_ops import rope
+    announce("block chain reference production geometry")
+    cos_h, sin_h = rope.visual_rope_half_tables((1, 30, 52), ref_video_frames=1)
+    cf, sf = rope.visual_rope_tables((1, 30, 52), ref_video_frames=1, temporal_ids=[1])
+    _full_block_check(4096, 32, 16384, 512, cos_h.cpu(), sin_h.cpu(),
+                      [(cf.float().cpu().contiguous(), sf.float().cpu().contiguous())], 505)
 
 
 def _small_block(seed, E=512, H=4, FFN=1536, hh=12, ww=20, T=32):
