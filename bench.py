@@ -66,13 +66,21 @@ def buffer_sets(bytes_per_set: int) -> int:
 
 
 class Rotation:
-    """Calls fn(set) on successive sets; each call during graph capture bakes in its own set."""
+    """Calls fn(set) on successive sets; each call during graph capture bakes in its own set.
+    With keep=True the tensor each call returns stays alive until the same set comes round
+    again, so an op that allocates its output writes a different buffer on every call of a
+    rotation (otherwise the allocator hands the same block back each time and the output can
+    stay resident in the MALL)."""
 
-    def __init__(self, sets, fn):
+    def __init__(self, sets, fn, keep=False):
         self.sets, self.fn, self.i = sets, fn, 0
+        self.kept = [None] * len(sets) if keep else None
 
     def __call__(self):
-        self.fn(self.sets[self.i % len(self.sets)])
+        j = self.i % len(self.sets)
+        r = self.fn(self.sets[j])
+        if self.kept is not None:
+            self.kept[j] = r
         self.i += 1
 
 
@@ -430,8 +438,8 @@ def bench_norm(steps, warmup):
     out = []
     b = 2 * M * N + 2 * M * N + 2 * 2 * N
     xs = [x0] + [x0.clone() for _ in range(buffer_sets(b) - 1)]
-    t = time_launches(Rotation(xs, lambda x: jo.fused_norm_scale_shift(x, None, None, sc, sh, "layer", 1e-6)),
-                      steps, warmup)
+    t = time_launches(Rotation(xs, lambda x: jo.fused_norm_scale_shift(x, None, None, sc, sh, "layer", 1e-6),
+                               keep=True), steps, warmup)
     out.append({"op": "fused_norm_scale_shift", "M": M, "N": N, "us": t * 1e6, "gbs": b / t / 1e9,
                 "frac_hbm_peak": b / t / 1e9 / PEAK_HBM_GBS, "algorithmic_bytes": b, "buffer_sets": len(xs)})
     for exact in (False, True):

