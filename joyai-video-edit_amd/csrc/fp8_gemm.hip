@@ -184,7 +184,8 @@ __device__ __forceinline__ void store_tile_lds(const v16f (&acc)[FN][FM], const 
         v = make_uint4(gated_pair<kBf16>(v.x, x.x, gv.x), gated_pair<kBf16>(v.y, x.y, gv.y),
                        gated_pair<kBf16>(v.z, x.z, gv.z), gated_pair<kBf16>(v.w, x.w, gv.w));
       }
-      *(uint4*)(C + (int64_t)m * ldc + n) = v;
+      typedef unsigned u32x4 __attribute__((ext_vector_type(4)));  // written once: non-temporal
+      __builtin_nontemporal_store((u32x4){v.x, v.y, v.z, v.w}, (u32x4*)(C + (int64_t)m * ldc + n));
     }
   }
 }
@@ -897,7 +898,9 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4p(
             const int m = mw + j * 32 + h * 16 + r, n = nw0 + c * 8;
             const uint32_t off = (m < M && n < N) ? (uint32_t)(((int64_t)m * ldc + n) * 2) : 0x80000000u;
             typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-            __builtin_amdgcn_raw_buffer_store_b128((u32x4){v.x, v.y, v.z, v.w}, crs, (int)off, 0, 0);
+            // cache policy 2 = nt: the output is written once (non-temporal stores measured 2.5 %
+            // faster over the cfg-2 GEMMs than default-policy stores)
+            __builtin_amdgcn_raw_buffer_store_b128((u32x4){v.x, v.y, v.z, v.w}, crs, (int)off, 0, 2);
           }
           asm volatile("" ::: "memory");
         }
