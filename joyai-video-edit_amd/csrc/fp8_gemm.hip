@@ -985,13 +985,21 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4k(
   operand_rows<IA, IW, KS>(A, W, M, N, K, job, wave, lane, pa, pw);
 
   v4i stg[U][LOADS];
+  // With a single row of tiles every W byte is read by one workgroup only: non-temporal loads
+  // (M 64 x N 15360: 21.2 -> 20.1 us). With several, workgroups of one XCD share W through L2.
+  const bool w_once = tiles_m == 1;
   auto gload = [&](auto bc, int kt) {
     constexpr int B = decltype(bc)::value;
     const int64_t koff = (int64_t)min(kt, nk - 1) * KS;
 #pragma unroll
     for (int i = 0; i < IA; ++i) stg[B][i] = *(const v4i*)(pa[i] + koff);
+    if (w_once) {
 #pragma unroll
-    for (int i = 0; i < IW; ++i) stg[B][IA + i] = *(const v4i*)(pw[i] + koff);
+      for (int i = 0; i < IW; ++i) stg[B][IA + i] = __builtin_nontemporal_load((const v4i*)(pw[i] + koff));
+    } else {
+#pragma unroll
+      for (int i = 0; i < IW; ++i) stg[B][IA + i] = *(const v4i*)(pw[i] + koff);
+    }
   };
   auto lwrite = [&](auto bc, int slot) {
     constexpr int B = decltype(bc)::value;
