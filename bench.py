@@ -475,13 +475,17 @@ def bench_block(steps, warmup, n_cached=2):
     cos, sin = rope_3d_half_tables(3, 45, 80, (44, 42, 42), 10000.0, device=dev, frame_ids=frames)
     ring = KVRing(RING_SLOTS, L_TOK, HEADS, HEAD_DIM, dev)
     cached = []
+    # one full-width table over every cached token, cut into the chunks' rows (the reference builds
+    # cached_freqs_cis once per forward for all blocks, dit.py:1196-1217)
+    cf_all, sf_all = rotary_pos_embed_3d(torch.arange(0, 3 * n_cached), 45, 80, (44, 42, 42), 10000.0)
+    cf_all, sf_all = cf_all.contiguous().to(dev), sf_all.contiguous().to(dev)
     for c in range(n_cached):
         slot = RING_SLOTS - 1 - c
         ring.k[slot].normal_()
         ring.v[slot].normal_()
         ring.lengths[slot] = L_TOK
-        cf, sf = rotary_pos_embed_3d(torch.arange(3 * c, 3 * c + 3), 45, 80, (44, 42, 42), 10000.0)
-        cached.append(CachedChunk(slot, cf.contiguous().to(dev), sf.contiguous().to(dev)))
+        rows = slice(c * L_TOK, (c + 1) * L_TOK)
+        cached.append(CachedChunk(slot, cf_all[rows], sf_all[rows]))
     stages = ["qkv", "qkv_norm_rope", "cached_kv", "joint_pack", "attention", "proj_ffn"]
     stream = torch.cuda.current_stream()
     ev = {}

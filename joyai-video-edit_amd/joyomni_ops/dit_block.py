@@ -119,6 +119,18 @@ class CachedChunk:
     sin: Optional[torch.Tensor] = None
 
 
+def _adjacent_rows(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """Rows of a followed by rows of b: a view when b's rows follow a's in one contiguous buffer
+    (chunks cut from one table of every cached token, as the reference builds ``cached_freqs_cis``,
+    ``dit.py:1196-1217``), else a copy."""
+    if (a.is_contiguous() and b.is_contiguous() and a.dtype == b.dtype and a.device == b.device
+            and a.dim() == 2 and b.dim() == 2 and a.shape[1] == b.shape[1]
+            and b.data_ptr() == a.data_ptr() + a.numel() * a.element_size()
+            and a.untyped_storage().data_ptr() == b.untyped_storage().data_ptr()):
+        return a.as_strided((a.shape[0] + b.shape[0], a.shape[1]), (a.shape[1], 1))
+    return torch.cat([a, b])
+
+
 class QuantizedDoubleStreamBlock:
     """The quantised chain of one two-stream MMDiT block (see the module docstring)."""
 
@@ -208,8 +220,8 @@ class QuantizedDoubleStreamBlock:
             pair = i + 1 < len(cached) and ring.pre_rope[cached[i + 1].slot]
             seg = cached[i:i + 2] if pair else [c0]
             n = sum(ring.lengths[c.slot] for c in seg)
-            cos = torch.cat([c.cos for c in seg]) if pair else c0.cos
-            sin = torch.cat([c.sin for c in seg]) if pair else c0.sin
+            cos = _adjacent_rows(c0.cos, seg[1].cos) if pair else c0.cos
+            sin = _adjacent_rows(c0.sin, seg[1].sin) if pair else c0.sin
             k1 = ring.key(seg[1].slot) if pair else None
             v1 = ring.value(seg[1].slot) if pair else None
             fused_cached_kv_pack_out(ring.key(c0.slot), ring.value(c0.slot), k1, v1, cos, sin,

@@ -68,3 +68,19 @@ def test_write_bounds():
         check(40, r, 1, [], 40)
     with pytest.raises(ValueError, match="need a KV ring"):
         check(24, None, 1, [], 24)
+
+
+def test_adjacent_cached_tables_are_joined_without_a_copy():
+    """Two chunks' tables cut from one table of every cached token are joined as a view; any other
+    pair (reversed, separate buffers) is copied, and both give the rows of a then b."""
+    from joyomni_ops.dit_block import _adjacent_rows
+    full = torch.arange(12 * 4, dtype=torch.float32).reshape(12, 4)
+    a, b = full[:5], full[5:]
+    v = _adjacent_rows(a, b)
+    assert v.data_ptr() == full.data_ptr() and torch.equal(v, full)
+    r = _adjacent_rows(b, a)
+    assert r.data_ptr() != full.data_ptr() and torch.equal(r, torch.cat([b, a]))
+    c = _adjacent_rows(a.clone(), b.clone())
+    assert torch.equal(c, full)
+    gap = _adjacent_rows(full[:4], full[5:])
+    assert torch.equal(gap, torch.cat([full[:4], full[5:]]))

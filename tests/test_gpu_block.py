@@ -147,7 +147,7 @@ def _full_block_check(E, H, FFN, T, cos_h, sin_h, cached_tables, seed):
         ring.v[slot].copy_(val)
         ring.lengths[slot] = L
         cached.append(CachedChunk(slot, cf.to(DEV), sf.to(DEV)))
-        cached_cpu.append((kpre, val, cf, sf))
+        cached_cpu.append((kpre, val, cf.cpu(), sf.cpu()))
     out_img, out_txt = blk.forward(img.to(DEV), txt.to(DEV), vec.to(DEV), cos_h.to(DEV), sin_h.to(DEV),
                                    ring=ring, write_slot=0, cached=cached)
     torch.cuda.synchronize()
@@ -193,7 +193,10 @@ def test_block_chain_full_size_cfg4():
     announce("block chain full size cfg4")
     hh, ww = 45, 80
     cos_h, sin_h = _half_tables([6, 7, 8], hh, ww)      # current chunk after two cached chunks of 3 frames
-    cached = [_full_tables([3 * i, 3 * i + 1, 3 * i + 2], hh, ww) for i in range(2)]
+    # the two chunks' tables are rows of one table over all cached tokens (joined without a copy)
+    cf, sf = (t.to(DEV) for t in _full_tables(list(range(6)), hh, ww))
+    n = 3 * hh * ww
+    cached = [(cf[:n], sf[:n]), (cf[n:], sf[n:])]
     _full_block_check(5120, 40, 13824, 512, cos_h, sin_h, cached, 404)
 
 
