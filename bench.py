@@ -1,6 +1,6 @@
 """Benchmark of the MI355X quantised DiT hot path (one JSON line on stdout).
 
-Headline (``value``): BASELINE cfg 1 -- fused QKV split + per-head q/k RMSNorm +
+Headline (``value``): benchmark cfg 1 -- fused QKV split + per-head q/k RMSNorm +
 3-D RoPE + 4-slot KV-ring write over L=10800 tokens, 40x128 heads, in GB/s of
 algorithmic HBM traffic. One step = one launch over the whole chunk, inputs
 resident in HBM. Also reported in the same line: the cfg 2 FP8 GEMM sweep at
@@ -223,7 +223,7 @@ def bench_gemm(steps, warmup):
 
 
 def bench_cfg0(steps, warmup):
-    """BASELINE cfg 0: one Fp8Linear forward (per-token activation quant + FP8 GEMM + bias) at
+    """Benchmark cfg 0: one Fp8Linear forward (per-token activation quant + FP8 GEMM + bias) at
     256 x 4096 -> 4096, the shape the CPU baseline times; W streams from HBM (rotated copies)."""
     import torch
     import joyomni_ops as jo
@@ -456,7 +456,7 @@ def bench_norm(steps, warmup):
 
 
 def bench_block(steps, warmup, n_cached=2):
-    """BASELINE cfg 4: one two-stream MMDiT block's quantised chain, video 10800 + condition 512
+    """Benchmark cfg 4: one two-stream MMDiT block's quantised chain, video 10800 + condition 512
     tokens, hidden 5120, 40 x 128 heads, FFN 13824, random-init weights; the video chunk's K/V go
     into ring slot 0 and the block attends to ``n_cached`` cached chunks of 10800 tokens read from
     other ring slots (rotate-on-read). Per-stage device time from HIP events on the launch stream;
@@ -525,7 +525,7 @@ def bench_block(steps, warmup, n_cached=2):
 
 
 def bench_attention(steps, warmup):
-    """The block's joint attention core (SURVEY f4, dit.py:154-167): video 10800 + condition 512
+    """The block's joint attention core (dit.py:154-167): video 10800 + condition 512
     queries over 2 cached chunks + video + condition = 32912 keys, 40 heads x 128, bf16. This
     build's kernel (joy_attention_fwd, reading the token-major joint operands in place) vs the
     reference's own call, F.scaled_dot_product_attention on the transposed views (ROCm backend of
@@ -596,7 +596,7 @@ def cpu_baseline_gemm():
     from oracle import torch_path
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    Ms, K, N = 256, 4096, 4096  # BASELINE cfg 0
+    Ms, K, N = 256, 4096, 4096  # benchmark cfg 0
     g = torch.Generator().manual_seed(0)
     x = torch.randn(Ms, K, generator=g)
     x[:, torch.randperm(K, generator=g)[: K // 200]] *= 20

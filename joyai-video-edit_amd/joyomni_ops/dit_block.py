@@ -34,7 +34,7 @@ per stream (video "img", condition "txt"), with ``mod = table + vec`` split into
 
 Activation quantiser rounding per K follows the reference's ROCm path
 (``fp8_linear.py:57-74``): reciprocal-multiply below K = 8192, division above.
-Weights are random-initialised with the BASELINE distributions (there are no
+Weights are random-initialised with the benchmark distributions (there are no
 checkpoints here): Linear weights N(0, 0.02), biases N(0, 0.01), q/k norm weights
 N(1, 0.1), modulation table N(0, 1)/sqrt(hidden) (``ModulateWan.__init__``).
 """
@@ -69,7 +69,7 @@ class StreamWeights:
 
 def random_stream_weights(hidden: int, heads: int, mlp_hidden: int, generator: torch.Generator,
                           device) -> StreamWeights:
-    """Random-init weights of one stream with the BASELINE distributions (drawn on the CPU)."""
+    """Random-init weights of one stream with the benchmark distributions (drawn on the CPU)."""
     D = hidden // heads
 
     def linear(k_in, k_out):

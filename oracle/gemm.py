@@ -12,7 +12,7 @@ rules) and its epilogue tree ``fp8_gemm.cu:99-136``::
 ``B`` is given as ``Wq[N, K]`` row-major, i.e. the (K, N) column-major matrix
 the reference passes (``fp8_linear.py:83-84``).
 
-``reference_fp32`` is the BASELINE tolerance reference: fp32
+``reference_fp32`` is the benchmark's tolerance reference: fp32
 dequantise-then-matmul ``(qa * sa) @ (qb * sb)^T + bias``.
 
 Pins (tests/test_oracle_gemm.py): brute-force triple loop on tiny inputs; a
@@ -71,7 +71,7 @@ def scaled_mm(qa_u8, qb_nk_u8, sa, sb, bias_u16=None, out_dtype: str = "bf16"):
 
 
 def reference_fp32(qa_u8, qb_nk_u8, sa, sb, bias_u16=None) -> np.ndarray:
-    """BASELINE tolerance reference: fp32 dequantise-then-matmul + bias."""
+    """The benchmark's tolerance reference: fp32 dequantise-then-matmul + bias."""
     a = dequant(qa_u8) * sa.astype(np.float32)[:, None]
     b = dequant(qb_nk_u8) * sb.astype(np.float32)[:, None]
     o = (a.astype(np.float64) @ b.astype(np.float64).T).astype(np.float32)

@@ -1,6 +1,6 @@
 """The reference's CPU-runnable torch code path for the hot path, restated (torch, CPU).
 
-TEST / BASELINE INFRASTRUCTURE ONLY -- see ``oracle/__init__.py``. ``bench.py``
+TEST / CPU-BASELINE INFRASTRUCTURE ONLY -- see ``oracle/__init__.py``. ``bench.py``
 times these functions on the host cores as the reported CPU baseline.
 
 * ``qkv_norm_rope_cache`` -- the reference's per-block sequence for one stream:
@@ -10,7 +10,7 @@ times these functions on the host cores as the reported CPU baseline.
   pre-RoPE K kept (``return_k_pre_rope``) and V compacted for the cache
   (``dit.py:131-137,446-451``), written into a ring slot.
 * ``fp8_linear`` -- ``_quantize_per_token_impl`` (``fp8_linear.py:38-43``) followed
-  by fp32 dequantise-then-matmul + bias -> bf16, the BASELINE GEMM reference
+  by fp32 dequantise-then-matmul + bias -> bf16, the benchmark's GEMM reference
   (row-wise ``torch._scaled_mm`` is not available on the CPU backend).
 """
 from __future__ import annotations

@@ -9,9 +9,9 @@ reference's own formulas, independently of the numpy/C oracle they pin:
   torch amax / division / clamp / e4m3fn cast; plus the reciprocal-multiply
   variant of joyomni_ops/csrc/per_token_quant_fp8_rocm.hip:72-77.
   Geometries: the reference test's M=67 with a zero row (test_parity_light.py:113-120,
-  K reduced to 512) and BASELINE cfg 0's outlier distribution (K reduced to 1024).
+  K reduced to 512) and benchmark cfg 0's outlier distribution (K reduced to 1024).
 * gemm_small.npz -- torch fp8 -> fp32 dequantisation and float64 matmul, the
-  fp32 dequantise-then-matmul reference of BASELINE cfg 0 at 48x256x40.
+  fp32 dequantise-then-matmul reference of benchmark cfg 0 at 48x256x40.
 * qk_norm_rope.npz -- the reference test's fp32 closed form ``ref_one``
   (test_parity_light.py:93-103) at B=1, L=16, H=4, D=128 with random bf16 tables.
 
@@ -60,7 +60,7 @@ def main() -> None:
     x = torch.randn(67, 512, generator=g).to(torch.bfloat16)
     x[0].zero_()
     make_quant("quant_m67_zero_row.npz", x)
-    # BASELINE cfg 0 distribution: N(0,1), 0.5% of channels x20
+    # benchmark cfg 0 distribution: N(0,1), 0.5% of channels x20
     K = 1024
     x = torch.randn(32, K, generator=g)
     cols = torch.randperm(K, generator=g)[: max(1, K // 200)]

@@ -27,7 +27,7 @@ def gen(seed: int) -> torch.Generator:
 
 
 def outlier_acts(M: int, K: int, g: torch.Generator) -> torch.Tensor:
-    """BASELINE cfg 0 activations: N(0,1) with 0.5% of channels scaled x20 (bf16)."""
+    """benchmark cfg 0 activations: N(0,1) with 0.5% of channels scaled x20 (bf16)."""
     x = torch.randn(M, K, generator=g)
     cols = torch.randperm(K, generator=g)[: max(1, K // 200)]
     x[:, cols] *= 20

@@ -186,7 +186,7 @@ def _full_tables(frames, hh, ww):
 
 
 def test_block_chain_full_size_cfg4():
-    """BASELINE cfg 4 at its workload: video 10800 tokens (3 x 45 x 80) + condition 512, hidden 5120,
+    """benchmark cfg 4 at its workload: video 10800 tokens (3 x 45 x 80) + condition 512, hidden 5120,
     40 x 128 heads, FFN 13824, 2 cached chunks of 10800 tokens in ring slots 2 and 3, the current
     chunk written to slot 0: persistent 256x256 GEMMs with the GELU and gated-residual epilogues,
     the attention grid over 32912 keys."""

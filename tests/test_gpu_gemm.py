@@ -1,6 +1,6 @@
 """GPU parity: FP8 row/column-scaled GEMM (+bias, +GELU-tanh), bit-exact where the
 result is fixed exactly, else max|err| <= 2e-2 * RMS(out) vs fp32
-dequantise-then-matmul (BASELINE tolerance) and <= 1 bf16 ulp vs the oracle's
+dequantise-then-matmul (the benchmark's tolerance) and <= 1 bf16 ulp vs the oracle's
 exact-accumulation epilogue for all but a vanishing fraction."""
 import numpy as np
 import pytest
@@ -276,7 +276,7 @@ def test_small_m_plans_exact_with_and_without_workspace(M, N, K):
 
 @pytest.mark.parametrize("M,N,K", [(64, 5120, 5120), (256, 5120, 5120), (512, 5120, 13824)])
 def test_small_m_split_random_within_tolerance(M, N, K):
-    """cfg-0 distributions through a split plan: BASELINE tolerance and the accumulation bound,
+    """cfg-0 distributions through a split plan: the benchmark's tolerance and the accumulation bound,
     and the split and unsplit launches agree to the same bound."""
     announce("gemm small-M split random", M, N, K)
     qa, sa, qw, sw, bias = quantized_problem(M, N, K, M + N + K)

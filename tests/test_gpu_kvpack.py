@@ -1,6 +1,6 @@
 """GPU parity: fused_joint_qkv_pack and fused_cached_kv_pack (HIP kernels) vs the
 oracle. Copied rows (img Q/K, cached K/V, every V) must be bit-exact; text-norm
-and rotated rows within 1e-2 relative (BASELINE) and at most 1 bf16 ulp from the
+and rotated rows within 1e-2 relative (the benchmark's tolerance) and at most 1 bf16 ulp from the
 oracle on all but 0.1 % of elements."""
 import numpy as np
 import pytest

@@ -1,6 +1,6 @@
 """GPU parity: q/k RMSNorm + RoPE (in-place reference op) and the fused QKV
 split + norm + RoPE + KV-ring write, vs the oracle. Tolerance: 1e-2 relative
-(BASELINE) and at most 1 bf16 ulp from the oracle's correctly rounded result
+(the benchmark's tolerance) and at most 1 bf16 ulp from the oracle's correctly rounded result
 for all but 0.1% of elements; V copies and untouched ring slots bit-exact."""
 import numpy as np
 import pytest
