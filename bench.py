@@ -591,6 +591,50 @@ def cpu_baseline_qkv():
                       f"torch CPU restatement of sgl_fused_ops.py:170-199 + cache copy"}
 
 
+def cpu_baselines_more():
+    """Host-core timings (torch CPU restatements, oracle/torch_path.py) of the other hot-path kernels
+    on bounded samples of their bench workloads, reported beside the GPU figures."""
+    import torch
+    import torch.nn.functional as F
+    from oracle import torch_path
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(5)
+
+    def median_time(fn, reps=5):
+        fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return sorted(ts)[len(ts) // 2]
+
+    out = {}
+    M, K = L_TOK, E
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    t = median_time(lambda: torch_path.quantize_per_token_rounding(x, True))
+    out["act_quant"] = {"value": quant_bytes(M, K) / t / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
+                        "us": t * 1e6, "sample": f"full M {M} x K {K}, division (fp8_linear.py:38-43), median of 5"}
+    sc = (0.2 * torch.randn(1, K, generator=g)).to(torch.bfloat16)
+    sh = (0.2 * torch.randn(1, K, generator=g)).to(torch.bfloat16)
+    t = median_time(lambda: torch_path._layernorm_modulate_ref(x, sh, sc, 1e-6))
+    b = 2 * M * K + 2 * M * K + 2 * 2 * K
+    out["adaln_norm"] = {"value": b / t / 1e9, "unit": "GB/s", "cores": cores, "kind": "port", "us": t * 1e6,
+                         "sample": f"full M {M} x N {K}, fp32 layer_norm * (1 + scale) + shift -> bf16, median of 5"}
+    del x
+    Lq, Lk = 1024, 3 * L_TOK + 512  # one head's 1024 queries over the whole joint key sequence
+    q = torch.randn(1, 1, Lq, HEAD_DIM, generator=g).to(torch.bfloat16)
+    k = torch.randn(1, 1, Lk, HEAD_DIM, generator=g).to(torch.bfloat16)
+    v = torch.randn(1, 1, Lk, HEAD_DIM, generator=g).to(torch.bfloat16)
+    t = median_time(lambda: F.scaled_dot_product_attention(q.float(), k.float(), v.float()), reps=3)
+    out["attention"] = {"value": 4 * Lq * Lk * HEAD_DIM / t / 1e12, "unit": "TFLOP/s", "cores": cores,
+                        "kind": "port", "us": t * 1e6,
+                        "sample": f"1 head, {Lq} queries x {Lk} keys x {HEAD_DIM} (fp32 F.scaled_dot_product_attention "
+                                  f"on the bf16 inputs, dit.py:154-167), median of 3"}
+    return out
+
+
 def cpu_baseline_gemm():
     import torch
     from oracle import torch_path
@@ -720,6 +764,8 @@ def main():
             rec["cpu_baseline"] = cpu_baseline_qkv()
         if args.only in ("all", "gemm", "cfg0"):
             rec["cpu_baseline_gemm"] = cpu_baseline_gemm()
+        if args.only == "all":
+            rec["cpu_baselines_more"] = cpu_baselines_more()
     print(json.dumps(rec), flush=True)
 
 
