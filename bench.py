@@ -52,6 +52,7 @@ def quant_bytes(M, K) -> int:
 
 
 EAGER = False  # --eager: plain launches instead of one HIP graph (for counter runs)
+STEADY_S = 0.05  # seconds of back-to-back replays before each timed replay
 
 # MI355X has a 256 MiB memory-side cache (MALL) in front of HBM: a launch whose working set fits
 # in it, replayed on the same buffers, is partly served from it. Memory-bound benchmarks whose
@@ -89,8 +90,12 @@ def time_launches(fn, steps: int, warmup: int):
 
     The `steps` launches are captured once into a HIP graph on a side stream and
     the graph is replayed between two events recorded on that same stream, so the
-    figure is device time without Python dispatch gaps. Falls back to eager
-    launches on the current stream if capture is refused.
+    figure is device time without Python dispatch gaps. Before the timed replay the
+    graph is replayed back to back for at least STEADY_S seconds: after any pause
+    (host-side set-up of the next case) the part takes ~30 ms of continuous load to
+    settle its clock, and a GEMM timed inside that window ran 10-20 % slower than
+    at steady state, which penalised whichever leg of a comparison ran first.
+    Falls back to eager launches on the current stream if capture is refused.
     """
     import torch
     for _ in range(warmup):
@@ -109,8 +114,13 @@ def time_launches(fn, steps: int, warmup: int):
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
         with torch.cuda.stream(stream):  # replay runs on the current stream
+            start.record(stream)
             graph.replay()  # warm replay
+            end.record(stream)
             torch.cuda.synchronize()
+            warm = max(0, min(400, int(STEADY_S / max(start.elapsed_time(end) / 1e3, 1e-6))))
+            for _ in range(warm):  # back to back until the clock has settled
+                graph.replay()
             start.record(stream)
             graph.replay()
             end.record(stream)
