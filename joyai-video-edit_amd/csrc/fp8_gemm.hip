@@ -611,22 +611,29 @@ __device__ __forceinline__ void static_for(F&& f) {
 // Persistent variant of the 256x256 bulk launch (plain and GELU epilogues): gridDim.x
 // workgroups (a multiple of 8, one per CU) each walk the tiles b, b + gridDim.x, ... of
 // the XCD-ordered grouped tile order. The operand ring runs on across tiles: during the
-// last 4 K steps of a tile the ring fetches the next tile's first 4 steps, so a new tile
+// last 2 K steps of a tile the ring fetches the next tile's first 2 steps, so a new tile
 // starts on data already in LDS, and the epilogue's stores drain while the next tile's
-// MFMAs run. Measured against the one-tile-per-workgroup launch on the cfg-2 shapes:
-// 2 % faster on QKV and the out-projection, equal on FFN-down (min of 4 runs each).
+// MFMAs run.
 //
-//   * K steps of 64 bytes, a ring of S = 4 slots (128 KiB); steps go through buffer
-//     loads straight into LDS (row offsets are 32-bit: M*K, N*K < 2^31).
+//   * K steps of 128 bytes in a ring of S = 2 slots of 64 KiB: every operand row of a step
+//     is one 128-byte request (with 64-byte steps and a 4-slot ring the same kernel made
+//     twice the L2 requests and ran 2-6 % slower on the cfg-2 GEMMs: QKV 748 -> 706 us,
+//     out-projection 260 -> 253, FFN-up + GELU 727 -> 681, FFN-down 636 -> 622, bit-identical).
+//     Step t (slot t & 1): the MFMAs of its first 64-byte half while the second half's
+//     fragments are read; wait for step t + 1 and one barrier; the DMA of step t + 2 into
+//     slot t & 1 (whose reads every wave has finished); the MFMAs of the second half while
+//     the first half of step t + 1 is read. A step's DMA thus has one step (32 MFMAs per
+//     wave) to land. Steps go through buffer loads straight into LDS (row offsets are
+//     32-bit: M*K, N*K < 2^31).
 //   * Per-tile column scales, bias and row scales arrive by one DMA per wave with the
-//     tile's first step into side_lds; the epilogue stages 16-row chunks of the wave's
+//     tile's step 2 into side_lds; the epilogue stages 16-row chunks of the wave's
 //     128x128 sub-tile through its own 4 KiB of stage_lds and stores 16-byte row segments
 //     with buffer stores (out-of-range lanes get an offset past the buffer, so every
 //     wave issues exactly NST stores per tile, whatever M and N).
 //   * vmcnt is in order on gfx9 for loads and stores alike, so each wait is a constant:
-//     W0 = 2 steps of DMAs in the steady state; after an epilogue the first three waits
-//     of the next tile also count the NST stores (and the side DMA) issued after the
-//     step they wait for.
+//     none of a step's own DMAs may be outstanding when the next step is read, except in
+//     a tile's first step, whose wait (for step 1, fetched during the previous tile) also
+//     counts the NST epilogue stores issued after it.
 //   * The DMAs are inline asm: the compiler does not track them (through the builtins
 //     it cannot tell an epilogue LDS access from the ring slots the DMAs write and
 //     waits for every DMA in flight). m0 is written only by those asm statements.
@@ -659,18 +666,17 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4p(
     const float* __restrict__ sb, const uint16_t* __restrict__ bias, uint16_t* __restrict__ C,
     int M, int N, int K, int64_t ldc, int tiles_m, int tiles_n, int group_m, int ntiles) {
   static_assert(kEpi == kEpiPlain || kEpi == kEpiGelu, "plain and GELU epilogues");
-  constexpr int BM = 256, BN = 256, KS = 64, NW = 4, S = 4;
+  constexpr int BM = 256, BN = 256, KS = 128, NW = 4, S = 2;
   constexpr int WTM = BM / 2, WTN = BN / 2, FM = WTM / 32, FN = WTN / 32;
-  constexpr int RPI = 16, IA = BM / RPI / NW, IW = BN / RPI / NW, LOADS = IA + IW;
+  constexpr int CPR = KS / 16, RPL = 64 / CPR;  // 8 chunks per row, 8 rows per DMA instruction
+  constexpr int IA = BM / RPL / NW, IW = BN / RPL / NW, LOADS = IA + IW;
   constexpr int A_BYTES = BM * KS, SLOT = (BM + BN) * KS;
   constexpr int NMFMA = FM * FN, NREAD = 2 * (FM + FN);
-  constexpr int W0 = (S - 2) * LOADS;
-  constexpr int NST = WTM * WTN * 2 / 1024;  // epilogue stores per wave and tile
-  constexpr int CROWS = 16;                  // rows per staging chunk
-  constexpr int STAGE = CROWS * WTN * 2;     // bytes per wave and chunk
+  constexpr int NST = WTM * WTN * 2 / 1024;
+  constexpr int CROWS = 16;
+  constexpr int STAGE = CROWS * WTN * 2;
   static_assert(S * SLOT + 4096 + NW * STAGE <= 160 * 1024, "LDS");
-  static_assert((S - 1) * LOADS + NST < 64, "vmcnt range");
-  // three objects: the compiler sees that no DMA writes the staging area
+  static_assert(LOADS + NST + 1 < 64, "vmcnt range");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[S * SLOT];
   __shared__ __attribute__((aligned(1024))) uint8_t side_lds[4096];
   __shared__ __attribute__((aligned(1024))) uint8_t stage_lds[NW * STAGE];
@@ -680,9 +686,8 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4p(
   const int wm = wave >> 1, wn = wave & 1;
   const int frow = lane & 31, g = lane >> 5;
   const int fsw = swz_rows<KS>(frow);
-  const int off0 = ((2 * g) ^ fsw) * 16, off1 = ((2 * g + 1) ^ fsw) * 16;
   const int a_row0 = (wm * WTM + frow) * KS, w_row0 = A_BYTES + (wn * WTN + frow) * KS;
-  const int nk = K / KS;
+  const int nk = K / KS;  // even (K % 256 == 0)
   const int P = gridDim.x;
   const bool has_bias = bias != nullptr;
   const __amdgpu_buffer_rsrc_t crs =
@@ -695,11 +700,8 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4p(
   TileCoord tc = map_tile(b, ntiles, tiles_m, tiles_n, group_m, 0);
   int m0 = tc.tm * BM, n0 = tc.tn * BN;
 
-  // per-lane 32-bit offsets of the operand rows of the tile at (mm, nn), logical chunk
-  // swizzled as in operand_rows
   uint32_t oa[IA], ow[IW];
   auto set_rows = [&](int mm, int nn) {
-    constexpr int CPR = KS / 16, RPL = 64 / CPR;
     const int lrow = lane / CPR, lchunk = lane % CPR;
 #pragma unroll
     for (int i = 0; i < IA; ++i) {
@@ -720,9 +722,6 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4p(
 #pragma unroll
     for (int i = 0; i < IW; ++i) dma_buf16(base + A_BYTES + (wave * IW + i) * 1024, ow[i], wrs, koff);
   };
-  // side operands of a tile, one 16-byte DMA per lane and wave: row scales (wave 0),
-  // column scales (1), bias (2, or column scales again without bias), a spare copy (3);
-  // M % 4 == 0 keeps the clamped row-scale reads in bounds
   auto issue_side = [&](int mm, int nn) {
     const int lr = min(lane, (M - mm) / 4 - 1), lc = min(lane, (N - nn) / 4 - 1), lb = min(lane, (N - nn) / 8 - 1);
     const void* ps = sa + mm + 4 * lr;
@@ -733,21 +732,23 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4p(
   };
 
   v16f acc[FN][FM];
-  v8i fw0[FN], fa0[FM], fw1[FN], fa1[FM];
-  auto read_frags = [&](int slot, v8i (&fw)[FN], v8i (&fa)[FM]) {
+  v8i fwx[FN], fax[FM], fwy[FN], fay[FM];
+  // fragments of 64-byte half h of the step in `slot`
+  auto read_frags = [&](int slot, int h, v8i (&fw)[FN], v8i (&fa)[FM]) {
     const uint8_t* base = lds + slot * SLOT;
+    const int o0 = ((4 * h + 2 * g) ^ fsw) * 16, o1 = ((4 * h + 2 * g + 1) ^ fsw) * 16;
 #pragma unroll
     for (int f = 0; f < FN; ++f) {
       const uint8_t* r = base + w_row0 + f * 32 * KS;
-      const v4i lo = *(const v4i*)(r + off0);
-      const v4i hi = *(const v4i*)(r + off1);
+      const v4i lo = *(const v4i*)(r + o0);
+      const v4i hi = *(const v4i*)(r + o1);
       fw[f] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
     }
 #pragma unroll
     for (int f = 0; f < FM; ++f) {
       const uint8_t* r = base + a_row0 + f * 32 * KS;
-      const v4i lo = *(const v4i*)(r + off0);
-      const v4i hi = *(const v4i*)(r + off1);
+      const v4i lo = *(const v4i*)(r + o0);
+      const v4i hi = *(const v4i*)(r + o1);
       fa[f] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
     }
   };
@@ -762,12 +763,18 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4p(
           acc[i][j] = mfma_32x32x64_fp8(fw[i], fa[j], acc[i][j]);
       }
   };
-  // iteration of K step kt (slot kt % S): wait + barrier, DMA of the step S ahead (byte
-  // offset koff in the rows set by set_rows) into this slot, fragment reads of step kt + 1
-  // (not in a tile's last iteration), MFMAs of step kt
-  auto iteration = [&](auto wait, auto slot, auto zero, auto last, bool side, int koff, const v8i(&fw)[FN],
-                       const v8i(&fa)[FM], v8i(&nw)[FN], v8i(&na)[FM]) {
-    constexpr int SL = decltype(slot)::value;
+  using F = std::false_type;
+  using T_ = std::true_type;
+  // one 128-byte step in slot SL: half 0 (fragments X) with the reads of half 1 (into Y); wait for
+  // the next step (outstanding vmcnt `wait`), barrier; DMA `koff` into this slot (and the side
+  // operands); half 1 (Y) with the reads of the next step's half 0 (into X; after the last tile
+  // they read a slot nobody uses, which keeps one code path and no spills)
+  auto step = [&](auto slotc, auto zero, auto wait, bool side, int koff) {
+    constexpr int SL = decltype(slotc)::value;
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(SL, 1, fwy, fay);
+    mfmas(fwx, fax, zero);
+    sched_pattern<0, NMFMA, NREAD, 0>();
     __builtin_amdgcn_sched_barrier(0);
     wait_vmcnt_lgkm0<decltype(wait)::value>();
     block_barrier();
@@ -775,50 +782,33 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4p(
     if (side) issue_side(m0, n0);
     issue(SL, koff);
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (!decltype(last)::value) read_frags((SL + 1) % S, nw, na);
-    mfmas(fw, fa, zero);
-    if constexpr (decltype(last)::value) {
-      sched_pattern<0, NMFMA, 0, 0>();
-    } else {
-      sched_pattern<0, NMFMA, NREAD, 0>();
-    }
+    read_frags(SL ^ 1, 0, fwx, fax);
+    mfmas(fwy, fay, F{});
+    sched_pattern<0, NMFMA, NREAD, 0>();
     __builtin_amdgcn_sched_barrier(0);
   };
-  using F = std::false_type;
-  using T_ = std::true_type;
 
-#pragma unroll
-  for (int s = 0; s < S; ++s) issue(s, s * KS);
+  // prologue: steps 0 and 1 of the first tile, fragments of step 0's first half
+  issue(0, 0);
+  issue(1, KS);
+  wait_vmcnt<LOADS>();
+  block_barrier();
+  read_frags(0, 0, fwx, fax);
   bool first = true;
   for (;;) {
-    // fragments of step 0 (slot 0): after a tile, its NST stores were issued after the DMAs
-    // of steps 0..3
+    // step 0: its wait is for step 1, issued before the previous tile's NST epilogue stores
     if (first) {
-      wait_vmcnt<(S - 1) * LOADS>();
+      step(IC<0>{}, T_{}, IC<0>{}, true, 2 * KS);
     } else {
-      wait_vmcnt<(S - 1) * LOADS + NST>();
+      step(IC<0>{}, T_{}, IC<NST>{}, true, 2 * KS);
     }
-    block_barrier();
-    read_frags(0, fw0, fa0);
-    // steps 0..3 (DMAs of steps 4..7, the side operands with step 4, accumulators from zero)
-    if (first) {
-      iteration(IC<W0>{}, IC<0>{}, T_{}, F{}, true, 4 * KS, fw0, fa0, fw1, fa1);
-      iteration(IC<W0>{}, IC<1>{}, F{}, F{}, false, 5 * KS, fw1, fa1, fw0, fa0);
-      iteration(IC<W0>{}, IC<2>{}, F{}, F{}, false, 6 * KS, fw0, fa0, fw1, fa1);
-    } else {
-      iteration(IC<W0 + NST>{}, IC<0>{}, T_{}, F{}, true, 4 * KS, fw0, fa0, fw1, fa1);
-      iteration(IC<W0 + NST + 1>{}, IC<1>{}, F{}, F{}, false, 5 * KS, fw1, fa1, fw0, fa0);
-      iteration(IC<W0 + NST + 1>{}, IC<2>{}, F{}, F{}, false, 6 * KS, fw0, fa0, fw1, fa1);
-    }
-    iteration(IC<W0>{}, IC<3>{}, F{}, F{}, false, 7 * KS, fw1, fa1, fw0, fa0);
     first = false;
-    for (int kt = 4; kt + S < nk; kt += 4) {
-      iteration(IC<W0>{}, IC<0>{}, F{}, F{}, false, (kt + 4) * KS, fw0, fa0, fw1, fa1);
-      iteration(IC<W0>{}, IC<1>{}, F{}, F{}, false, (kt + 5) * KS, fw1, fa1, fw0, fa0);
-      iteration(IC<W0>{}, IC<2>{}, F{}, F{}, false, (kt + 6) * KS, fw0, fa0, fw1, fa1);
-      iteration(IC<W0>{}, IC<3>{}, F{}, F{}, false, (kt + 7) * KS, fw1, fa1, fw0, fa0);
+    step(IC<1>{}, F{}, IC<0>{}, false, 3 * KS);
+    for (int kt = 2; kt + 2 < nk; kt += 2) {
+      step(IC<0>{}, F{}, IC<0>{}, false, (kt + 2) * KS);
+      step(IC<1>{}, F{}, IC<0>{}, false, (kt + 3) * KS);
     }
-    // last 4 steps: DMA the next tile's steps 0..3, or re-fetch this tile's last step into
+    // last two steps: DMA the next tile's steps 0 and 1, or re-fetch this tile's last step into
     // slots nobody reads again
     const int bn = b + P;
     const bool more = bn < ntiles;
@@ -832,10 +822,8 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4p(
       koffB = 0;
       dk = KS;
     }
-    iteration(IC<W0>{}, IC<0>{}, F{}, F{}, false, koffB, fw0, fa0, fw1, fa1);
-    iteration(IC<W0>{}, IC<1>{}, F{}, F{}, false, koffB + dk, fw1, fa1, fw0, fa0);
-    iteration(IC<W0>{}, IC<2>{}, F{}, F{}, false, koffB + 2 * dk, fw0, fa0, fw1, fa1);
-    iteration(IC<W0>{}, IC<3>{}, F{}, T_{}, false, koffB + 3 * dk, fw1, fa1, fw0, fa0);
+    step(IC<0>{}, F{}, IC<0>{}, false, koffB);
+    step(IC<1>{}, F{}, IC<0>{}, false, koffB + dk);
 
     // epilogue of tile (tm0, tn0)
     {
@@ -911,6 +899,7 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4p(
   }
   wait_vmcnt<0>();
 }
+
 
 // Instruction interleave of one deep-K iteration: N MFMAs with the R fragment reads
 // spread over all of them, the L global loads after the first L MFMAs and the L
@@ -1117,17 +1106,19 @@ hipError_t launch_4w(const GemmArgs& g, hipStream_t st) {
   }
   constexpr int D = 5;  // DMA ring depth
   const int bulk = T - rem;
-  // the persistent kernel takes the full rounds when there are at least two of them and its
-  // layout rules hold (K steps in groups of four, row scales read 4 at a time, 32-bit buffer
-  // offsets, a workgroup count that keeps the XCD mapping)
+  // the persistent kernel takes the full rounds (or a single partial one) when its layout
+  // rules hold (K steps in pairs of 128 bytes, row scales read 4 at a time, 32-bit buffer
+  // offsets, a workgroup count that keeps the XCD mapping); with fewer tiles than CUs it
+  // runs one tile per workgroup (1024 x 4096 -> 16384: 63 us vs 66 for the one-tile kernel,
+  // 3120 x 4096 -> 4096: 53 vs 56, 1560 x 4096 -> 12288: 90 vs 95 with the sub-tile tail)
   bool persistent = false;
   if constexpr (kEpi == kEpiPlain || kEpi == kEpiGelu) {
     constexpr int64_t kLim = 0x7fffffffLL;
     persistent = g.K % 256 == 0 && g.K >= 512 && g.M % 4 == 0 && (int64_t)g.M * g.K <= kLim &&
                  (int64_t)g.N * g.K <= kLim && ((int64_t)(g.M - 1) * g.ldc + g.N) * 2 <= kLim && P % 8 == 0 &&
-                 bulk >= 2 * P;
+                 bulk >= 1;
     if (persistent)
-      hipLaunchKernelGGL((fp8_gemm_4p<kBf16, kEpi>), dim3(P), dim3(256), 0, st, (const uint8_t*)g.A,
+      hipLaunchKernelGGL((fp8_gemm_4p<kBf16, kEpi>), dim3(bulk < P ? bulk : P), dim3(256), 0, st, (const uint8_t*)g.A,
                          (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N,
                          g.K, g.ldc, tiles_m, tiles_n, kGroupM, bulk);
   }

@@ -357,11 +357,11 @@ def test_reference_tuned_shapes(M, K, N):
 @pytest.mark.parametrize("M,kind", [(4096, "plain"), (4100, "plain"), (4100, "gelu"), (4096, "nobias"),
                                     (4100, "fp16")])
 def test_persistent_rounds_match_per_tile_launch(M, kind):
-    """At two or more full rounds of 256x256 tiles (and K % 256 == 0, M % 4 == 0) the bulk runs
-    as the persistent kernel; the same rows computed in two calls of fewer rounds take the
-    one-tile-per-workgroup kernel. Rows are independent and both sum each output's K products
-    in the same order, so the outputs must agree to the bit (M = 4100: a 4-row last tile row and
-    a sub-tile tail launch); sampled rows also hold the accumulation bound of the oracle."""
+    """With K % 256 == 0 and M % 4 == 0 the 256x256 bulk runs as the persistent kernel; the same
+    rows computed in two calls of odd row counts (M % 4 != 0) take the one-tile-per-workgroup
+    kernel. Rows are independent and both sum each output's K products in the same order, so
+    the outputs must agree to the bit (M = 4100: a 4-row last tile row and a sub-tile tail
+    launch); sampled rows also hold the accumulation bound of the oracle."""
     N, K = 8192, 512
     announce("gemm persistent", M, N, K, kind)
     qa, sa, qw, sw, bias = quantized_problem(M, N, K, 4242 + M)
@@ -371,7 +371,8 @@ def test_persistent_rounds_match_per_tile_launch(M, kind):
     b = None if kind == "nobias" else bias
     gelu = kind == "gelu"
     whole = u16(gemm(qa, qw, sa, sw, b, out_dtype, gelu).cpu())
-    h = M // 2
+    h = M // 2 + 1  # odd: both parts have M % 4 != 0
+    assert h % 4 != 0 and (M - h) % 4 != 0
     parts = [u16(gemm(qa[r0:r1], qw, sa[r0:r1], sw, b, out_dtype, gelu).cpu()) for r0, r1 in ((0, h), (h, M))]
     assert np.array_equal(whole, np.concatenate(parts, axis=0)), f"{kind}: persistent and per-tile outputs differ"
     if kind in ("plain", "nobias"):
