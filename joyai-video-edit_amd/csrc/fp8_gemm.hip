@@ -664,8 +664,8 @@ template <bool kBf16, int kEpi>
 __global__ __launch_bounds__(256, 1) void fp8_gemm_4p(
     const uint8_t* __restrict__ A, const uint8_t* __restrict__ W, const float* __restrict__ sa,
     const float* __restrict__ sb, const uint16_t* __restrict__ bias, uint16_t* __restrict__ C,
-    int M, int N, int K, int64_t ldc, int tiles_m, int tiles_n, int group_m, int ntiles) {
-  static_assert(kEpi == kEpiPlain || kEpi == kEpiGelu, "plain and GELU epilogues");
+    int M, int N, int K, int64_t ldc, int tiles_m, int tiles_n, int group_m, int ntiles, ResidualArgs res) {
+  static_assert(kEpi == kEpiPlain || kEpi == kEpiGelu || kEpi == kEpiResidual, "plain, GELU, gated residual");
   constexpr int BM = 256, BN = 256, KS = 128, NW = 4, S = 2;
   constexpr int WTM = BM / 2, WTN = BN / 2, FM = WTM / 32, FN = WTN / 32;
   constexpr int CPR = KS / 16, RPL = 64 / CPR;  // 8 chunks per row, 8 rows per DMA instruction
@@ -694,6 +694,11 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4p(
       __builtin_amdgcn_make_buffer_rsrc(C, 0, (int)(((int64_t)(M - 1) * ldc + N) * 2), 0x00020000);
   const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, (int)((int64_t)M * K), 0x00020000);
   const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc((void*)W, 0, (int)((int64_t)N * K), 0x00020000);
+  // gated residual (residual rows may be C itself) and gate; out-of-range offsets read zeros
+  const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)res.ptr, 0, kEpi == kEpiResidual ? (int)(((int64_t)(M - 1) * res.ld + N) * 2) : 0, 0x00020000);
+  const __amdgpu_buffer_rsrc_t grs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)res.gate, 0, kEpi == kEpiResidual ? N * 2 : 0, 0x00020000);
 
   int b = blockIdx.x;
   if (b >= ntiles) return;
@@ -767,9 +772,10 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4p(
   using T_ = std::true_type;
   // one 128-byte step in slot SL: half 0 (fragments X) with the reads of half 1 (into Y); wait for
   // the next step (outstanding vmcnt `wait`), barrier; DMA `koff` into this slot (and the side
-  // operands); half 1 (Y) with the reads of the next step's half 0 (into X; after the last tile
-  // they read a slot nobody uses, which keeps one code path and no spills)
-  auto step = [&](auto slotc, auto zero, auto wait, bool side, int koff) {
+  // operands); half 1 (Y) with the reads of the next step's half 0 (into X) unless it is the
+  // tile's last step (the next tile's first fragments are read after the epilogue, so that no
+  // fragment registers are live across it)
+  auto step = [&](auto slotc, auto zero, auto wait, bool side, int koff, auto nextc) {
     constexpr int SL = decltype(slotc)::value;
     __builtin_amdgcn_sched_barrier(0);
     read_frags(SL, 1, fwy, fay);
@@ -782,9 +788,13 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4p(
     if (side) issue_side(m0, n0);
     issue(SL, koff);
     __builtin_amdgcn_sched_barrier(0);
-    read_frags(SL ^ 1, 0, fwx, fax);
-    mfmas(fwy, fay, F{});
-    sched_pattern<0, NMFMA, NREAD, 0>();
+    if constexpr (decltype(nextc)::value) {
+      read_frags(SL ^ 1, 0, fwx, fax);
+      mfmas(fwy, fay, F{});
+      sched_pattern<0, NMFMA, NREAD, 0>();
+    } else {
+      mfmas(fwy, fay, F{});
+    }
     __builtin_amdgcn_sched_barrier(0);
   };
 
@@ -793,20 +803,21 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4p(
   issue(1, KS);
   wait_vmcnt<LOADS>();
   block_barrier();
-  read_frags(0, 0, fwx, fax);
   bool first = true;
   for (;;) {
+    // the first half of step 0 (in slot 0: landed before the last barrier)
+    read_frags(0, 0, fwx, fax);
     // step 0: its wait is for step 1, issued before the previous tile's NST epilogue stores
     if (first) {
-      step(IC<0>{}, T_{}, IC<0>{}, true, 2 * KS);
+      step(IC<0>{}, T_{}, IC<0>{}, true, 2 * KS, T_{});
     } else {
-      step(IC<0>{}, T_{}, IC<NST>{}, true, 2 * KS);
+      step(IC<0>{}, T_{}, IC<NST>{}, true, 2 * KS, T_{});
     }
     first = false;
-    step(IC<1>{}, F{}, IC<0>{}, false, 3 * KS);
+    step(IC<1>{}, F{}, IC<0>{}, false, 3 * KS, T_{});
     for (int kt = 2; kt + 2 < nk; kt += 2) {
-      step(IC<0>{}, F{}, IC<0>{}, false, (kt + 2) * KS);
-      step(IC<1>{}, F{}, IC<0>{}, false, (kt + 3) * KS);
+      step(IC<0>{}, F{}, IC<0>{}, false, (kt + 2) * KS, T_{});
+      step(IC<1>{}, F{}, IC<0>{}, false, (kt + 3) * KS, T_{});
     }
     // last two steps: DMA the next tile's steps 0 and 1, or re-fetch this tile's last step into
     // slots nobody reads again
@@ -822,8 +833,8 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4p(
       koffB = 0;
       dk = KS;
     }
-    step(IC<0>{}, F{}, IC<0>{}, false, koffB);
-    step(IC<1>{}, F{}, IC<0>{}, false, koffB + dk);
+    step(IC<0>{}, F{}, IC<0>{}, false, koffB, T_{});
+    step(IC<1>{}, F{}, IC<0>{}, false, koffB + dk, F{});
 
     // epilogue of tile (tm0, tn0)
     {
@@ -836,12 +847,31 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4p(
       const uint16_t* bias_l = (const uint16_t*)(side_lds + 2048);
       uint8_t* stage = stage_lds + wave * STAGE;
       const int mw = tm0 + wm * WTM, nw0 = tn0 + wn * WTN;
+      typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+      // the lane's 8 output columns in the read-back below are fixed for the tile
+      const int n_lane = nw0 + (lane_e & 15) * 8;
+      u32x4 gv = {0, 0, 0, 0};
+      if constexpr (kEpi == kEpiResidual)
+        gv = __builtin_amdgcn_raw_buffer_load_b128(grs, n_lane < N ? n_lane * 2 : 0x40000000, 0, 0);
 #pragma unroll
       for (int j = 0; j < FM; ++j) {
         // the lane's row er of MFMA tile j, all FN x 4 x 4 columns: scaled, biased, rounded
         // (and GELU on the rounded value, as the reference applies F.gelu to the GEMM output)
         int jz;  // re-read the column operands per chunk rather than holding them in registers
         asm volatile("v_mov_b32 %0, 0" : "=v"(jz));
+        // gated residual: the 8 residual row segments this lane stores for tile j, loaded before
+        // the chunk's arithmetic so that their latency overlaps it
+        u32x4 rx[2][CROWS / 4];
+        if constexpr (kEpi == kEpiResidual) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int k = 0; k < CROWS / 4; ++k) {
+              const int m = mw + j * 32 + h * 16 + k * 4 + (lane_e >> 4);
+              const uint32_t roff = (m < M && n_lane < N) ? (uint32_t)(((int64_t)m * res.ld + n_lane) * 2) : 0x80000000u;
+              rx[h][k] = __builtin_amdgcn_raw_buffer_load_b128(rrs, (int)roff, 0, 0);
+            }
+        }
         const float s_a = sa_l[wm * WTM + j * 32 + er];
         uint2 pk[FN][4];
 #pragma unroll
@@ -882,10 +912,14 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4p(
 #pragma unroll
           for (int k = 0; k < CROWS / 4; ++k) {
             const int r = k * 4 + (lane_e >> 4), c = lane_e & 15;
-            const uint4 v = *(const uint4*)(stage + r * (WTN * 2) + ((c ^ r) * 16));
+            uint4 v = *(const uint4*)(stage + r * (WTN * 2) + ((c ^ r) * 16));
             const int m = mw + j * 32 + h * 16 + r, n = nw0 + c * 8;
             const uint32_t off = (m < M && n < N) ? (uint32_t)(((int64_t)m * ldc + n) * 2) : 0x80000000u;
-            typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+            if constexpr (kEpi == kEpiResidual) {
+              const u32x4 x = rx[h][k];
+              v = make_uint4(gated_pair<kBf16>(v.x, x[0], gv[0]), gated_pair<kBf16>(v.y, x[1], gv[1]),
+                             gated_pair<kBf16>(v.z, x[2], gv[2]), gated_pair<kBf16>(v.w, x[3], gv[3]));
+            }
             // cache policy 2 = nt: the output is written once (non-temporal stores measured 2.5 %
             // faster over the cfg-2 GEMMs than default-policy stores)
             __builtin_amdgcn_raw_buffer_store_b128((u32x4){v.x, v.y, v.z, v.w}, crs, (int)off, 0, 2);
@@ -1112,15 +1146,15 @@ hipError_t launch_4w(const GemmArgs& g, hipStream_t st) {
   // runs one tile per workgroup (1024 x 4096 -> 16384: 63 us vs 66 for the one-tile kernel,
   // 3120 x 4096 -> 4096: 53 vs 56, 1560 x 4096 -> 12288: 90 vs 95 with the sub-tile tail)
   bool persistent = false;
-  if constexpr (kEpi == kEpiPlain || kEpi == kEpiGelu) {
+  if constexpr (kEpi == kEpiPlain || kEpi == kEpiGelu || kEpi == kEpiResidual) {
     constexpr int64_t kLim = 0x7fffffffLL;
     persistent = g.K % 256 == 0 && g.K >= 512 && g.M % 4 == 0 && (int64_t)g.M * g.K <= kLim &&
                  (int64_t)g.N * g.K <= kLim && ((int64_t)(g.M - 1) * g.ldc + g.N) * 2 <= kLim && P % 8 == 0 &&
-                 bulk >= 1;
+                 bulk >= 1 && (kEpi != kEpiResidual || ((int64_t)(g.M - 1) * g.ldr + g.N) * 2 <= kLim);
     if (persistent)
       hipLaunchKernelGGL((fp8_gemm_4p<kBf16, kEpi>), dim3(bulk < P ? bulk : P), dim3(256), 0, st, (const uint8_t*)g.A,
                          (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N,
-                         g.K, g.ldc, tiles_m, tiles_n, kGroupM, bulk);
+                         g.K, g.ldc, tiles_m, tiles_n, kGroupM, bulk, residual_args(g));
   }
   if (bulk > 0 && !persistent) {
     auto kern = fp8_gemm_4w<kBf16, kEpi, 256, 256, D>;

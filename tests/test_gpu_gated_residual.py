@@ -86,7 +86,10 @@ def test_exact_fp16():
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("M,N,K", [(64, 5120, 5120), (256, 15360, 1024), (4352, 4352, 256),
-                                   (2048, 5120, 13824), (777, 1000, 320)])
+                                   (2048, 5120, 13824), (777, 1000, 320),
+                                   # persistent 256x256 kernel (K % 256 == 0, M % 4 == 0): a whole
+                                   # round plus a sub-tile tail, and a single partial round
+                                   (4352, 4352, 512), (2600, 2304, 512)])
 def test_random_equals_addcmul_over_plain_gemm(dtype, M, N, K):
     """Large / every-launch-shape problems: the fused epilogue equals torch.addcmul applied to
     fp8_scaled_mm's own output (the same kernel tiling sums each output in the same order)."""
