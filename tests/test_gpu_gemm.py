@@ -245,13 +245,15 @@ def gemm_capi(qa_u8, qw_u8, sa, sw, bias_u16, out_dtype, workspace):
     return out, ws_bytes
 
 
-# Small-M plans (64-row tiles with 256-byte K steps for M <= 64, 128x128 / 128x256 tiles with
-# 128-byte K steps up to M = 512), each with and without a K split: ragged rows, partial
-# column tiles, uneven split ranges (300 x 2056 x 1664: 13 K steps in 3 splits), an odd
-# step count, and the block's 512-token FFN-down shape.
+# Small-M plans (64-row tiles with 256-byte K steps for M <= 64, or 512-byte steps when K is not
+# split; 128x128 / 128x256 tiles with 128-byte K steps up to M = 512), each with and without a
+# K split: ragged rows, partial column tiles, uneven split ranges (300 x 2056 x 1664: 13 K steps
+# in 3 splits), odd step counts (48 x 1544 x 2560: 5 steps of 512 bytes unsplit), and the
+# block's 512-token FFN-down shape.
 SMALL_M_PLAN_SHAPES = [(64, 5120, 5120), (33, 1032, 4096), (1, 264, 2048), (64, 15360, 256),
                        (200, 2056, 2048), (256, 5120, 1280), (129, 4104, 3072), (300, 2056, 1664),
-                       (512, 5120, 13824), (400, 12296, 1152), (320, 15360, 512), (512, 5120, 5120)]
+                       (512, 5120, 13824), (400, 12296, 1152), (320, 15360, 512), (512, 5120, 5120),
+                       (48, 1544, 2560)]
 
 
 @pytest.mark.parametrize("M,N,K", SMALL_M_PLAN_SHAPES)
