@@ -12,10 +12,16 @@
 // the reference block's projection + fused_add_gate pair (dit.py:525-528, 535-538;
 // sgl_fused_ops.py:302-305); residual and output may be the same buffer.
 //
-// Main kernel (fp8_gemm_4w, any M, N with K % 64 == 0):
-//  * 256 threads = 4 waves in 2x2, one wave per SIMD; macro tile 256x256 for the
-//    full rounds of the grid (one workgroup per CU), 256x128 or 128x128 sub-tiles
-//    for the tiles of the last, partial round, so more CUs share it;
+// Kernels by problem shape:
+//  * fp8_gemm_4p (K % 256 == 0, M % 4 == 0, M > 512): persistent 256x256 tiles, one
+//    workgroup per CU walking the whole rounds, 128-byte K steps through a 2-slot ring;
+//  * fp8_gemm_4k (M <= 512, and long-K GEMMs of less than one round): deep-K tiles
+//    with register-staged operands and optional split-K;
+//  * fp8_gemm_4w (any M, N with K % 64 == 0): one tile per workgroup; the sub-tiles of
+//    the last, partial round of a persistent launch and the remaining shapes. Its layout:
+//  * 256 threads = 4 waves in 2x2, one wave per SIMD; macro tile 256x256 (one workgroup
+//    per CU), 256x128 or 128x128 sub-tiles for the tiles of a last, partial round, so
+//    more CUs share it;
 //  * each wave accumulates its sub-tile as 32x32 tiles of
 //    v_mfma_f32_32x32x64_f8f6f4 (up to 256 fp32 accumulators per lane, AGPRs);
 //    the MFMA takes W as its "A" operand and the activation as "B";
