@@ -17,8 +17,11 @@
 //    workgroup per CU walking the whole rounds, 128-byte K steps through a 2-slot ring;
 //  * fp8_gemm_4k (M <= 512, and long-K GEMMs of less than one round): deep-K tiles
 //    with register-staged operands and optional split-K;
+//  * fp8_gemm_4h (K % 128 == 0): one 256x128 or 128x128 tile per workgroup with the
+//    persistent kernel's 128-byte K steps; the sub-tiles of the last, partial round and
+//    single-round GEMMs of <= 2048 rows that 256x128 tiles fill best;
 //  * fp8_gemm_4w (any M, N with K % 64 == 0): one tile per workgroup; the sub-tiles of
-//    the last, partial round of a persistent launch and the remaining shapes. Its layout:
+//    the last, partial round when K % 128 != 0 and the remaining shapes. Its layout:
 //  * 256 threads = 4 waves in 2x2, one wave per SIMD; macro tile 256x256 (one workgroup
 //    per CU), 256x128 or 128x128 sub-tiles for the tiles of a last, partial round, so
 //    more CUs share it;
@@ -941,6 +944,119 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4p(
 }
 
 
+// ---------------------------------------------------------------------------
+// One tile per workgroup with 128-byte K steps through an S-slot ring (the sub-tiles of a
+// persistent launch's last round, and single-round direct launches): the step schedule of
+// the persistent kernel -- MFMAs of a step's first 64-byte half while its second half is
+// read, a wait for the next step and one barrier, the DMA of step t + S into the slot just
+// finished, the second half's MFMAs while the next step's first half is read.
+// ---------------------------------------------------------------------------
+template <bool kBf16, int kEpi, int BM, int BN, int S>
+__global__ __launch_bounds__(256, 1) void fp8_gemm_4h(
+    const uint8_t* __restrict__ A, const uint8_t* __restrict__ W, const float* __restrict__ sa,
+    const float* __restrict__ sb, const uint16_t* __restrict__ bias, uint16_t* __restrict__ C,
+    int M, int N, int K, int64_t ldc, int tiles_m, int tiles_n, int group_m, int tile_base,
+    int sub_log2, ResidualArgs res) {
+  constexpr int KS = 128, NW = 4;
+  constexpr int WTM = BM / 2, WTN = BN / 2, FM = WTM / 32, FN = WTN / 32;
+  constexpr int CPR = KS / 16, RPL = 64 / CPR;  // 8 rows per DMA instruction
+  constexpr int IA = BM / RPL / NW, IW = BN / RPL / NW, LOADS = IA + IW;
+  constexpr int A_BYTES = BM * KS, SLOT = (BM + BN) * KS;
+  constexpr int NMFMA = FM * FN, NREAD = 2 * (FM + FN);
+  static_assert(IA * RPL * NW == BM && IW * RPL * NW == BN, "tile rows must split over waves");
+  static_assert(S >= 3 && (S - 1) * LOADS < 64, "vmcnt range");
+  constexpr int STAGE_BYTES = WTM * (WTN * 2 + 16);
+  constexpr int LDS_BYTES = S * SLOT > NW * STAGE_BYTES ? S * SLOT : NW * STAGE_BYTES;
+  static_assert(LDS_BYTES <= 160 * 1024, "LDS of one CU");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const TileJob job = decode_job<BM, BN, KS>(K, tiles_m, tiles_n, group_m, tile_base, sub_log2, 1);
+  const int nk = job.nk;
+  const uint8_t* pa[IA];
+  const uint8_t* pw[IW];
+  operand_rows<IA, IW, KS>(A, W, M, N, K, job, wave, lane, pa, pw);
+  auto issue = [&](int slot, int kt) {
+    const int64_t koff = (int64_t)min(kt, nk - 1) * KS;
+    uint8_t* base = lds + slot * SLOT;
+#pragma unroll
+    for (int i = 0; i < IA; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(pa[i] + koff),
+                                       (lds_void*)(base + (wave * IA + i) * 1024), 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < IW; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(pw[i] + koff),
+                                       (lds_void*)(base + A_BYTES + (wave * IW + i) * 1024), 16, 0, 0);
+  };
+
+  const int wm = wave >> 1, wn = wave & 1;
+  const int frow = lane & 31, g = lane >> 5;
+  const int fsw = swz_rows<KS>(frow);
+  const int a_row0 = (wm * WTM + frow) * KS, w_row0 = A_BYTES + (wn * WTN + frow) * KS;
+
+  v16f acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j) acc[i][j] = (v16f){};
+  v8i fwx[FN], fax[FM], fwy[FN], fay[FM];
+  // fragments of 64-byte half h of the step in `slot`
+  auto read_frags = [&](int slot, int h, v8i (&fw)[FN], v8i (&fa)[FM]) {
+    const uint8_t* base = lds + slot * SLOT;
+    const int o0 = ((4 * h + 2 * g) ^ fsw) * 16, o1 = ((4 * h + 2 * g + 1) ^ fsw) * 16;
+#pragma unroll
+    for (int f = 0; f < FN; ++f) {
+      const uint8_t* r = base + w_row0 + f * 32 * KS;
+      const v4i lo = *(const v4i*)(r + o0);
+      const v4i hi = *(const v4i*)(r + o1);
+      fw[f] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+#pragma unroll
+    for (int f = 0; f < FM; ++f) {
+      const uint8_t* r = base + a_row0 + f * 32 * KS;
+      const v4i lo = *(const v4i*)(r + o0);
+      const v4i hi = *(const v4i*)(r + o1);
+      fa[f] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+  };
+  auto mfmas = [&](const v8i (&fw)[FN], const v8i (&fa)[FM]) {
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j) acc[i][j] = mfma_32x32x64_fp8(fw[i], fa[j], acc[i][j]);
+  };
+
+  // prologue: steps 0 .. S-1 into slots 0 .. S-1, the first half of step 0
+#pragma unroll
+  for (int s = 0; s < S; ++s) issue(s, s);
+  wait_vmcnt<(S - 1) * LOADS>();
+  block_barrier();
+  read_frags(0, 0, fwx, fax);
+  int slot = 0;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int next = slot + 1 == S ? 0 : slot + 1;
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(slot, 1, fwy, fay);
+    mfmas(fwx, fax);
+    sched_pattern<0, NMFMA, NREAD, 0>();
+    __builtin_amdgcn_sched_barrier(0);
+    // step kt + 1 has landed (steps kt + 2 .. kt + S - 1 may still be in flight) and every wave
+    // has read this slot: refill it with step kt + S (past the end, the last step again)
+    wait_vmcnt_lgkm0<(S - 2) * LOADS>();
+    block_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    issue(slot, kt + S);
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(next, 0, fwx, fax);  // past the last step: a slot nobody uses
+    mfmas(fwy, fay);
+    sched_pattern<0, NMFMA, NREAD, 0>();
+    __builtin_amdgcn_sched_barrier(0);
+    slot = next;
+  }
+  finish_tile<kBf16, kEpi, BM, BN>(acc, job, lds, wave, lane, M, N, sa, sb, bias, C, ldc, res, nullptr);
+}
+
 // Instruction interleave of one deep-K iteration: N MFMAs with the R fragment reads
 // spread over all of them, the L global loads after the first L MFMAs and the L
 // LDS writes after the last L.
@@ -1170,15 +1286,25 @@ hipError_t launch_4w(const GemmArgs& g, hipStream_t st) {
   }
   if (rem > 0) {
     if (sub_log2 == 2) {
-      auto kern = fp8_gemm_4w<kBf16, kEpi, 128, 128, D>;
-      hipLaunchKernelGGL(kern, dim3(rem << 2), dim3(256), 0, st, (const uint8_t*)g.A, (const uint8_t*)g.W,
-                         g.scales_a, g.scales_b, (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N, g.K, g.ldc,
-                         tiles_m, tiles_n, kGroupM, bulk, 2, residual_args(g), nullptr, 1);
+      if (g.K % 128 == 0)
+        hipLaunchKernelGGL((fp8_gemm_4h<kBf16, kEpi, 128, 128, 4>), dim3(rem << 2), dim3(256), 0, st,
+                           (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias,
+                           (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tiles_m, tiles_n, kGroupM, bulk, 2, residual_args(g));
+      else
+        hipLaunchKernelGGL((fp8_gemm_4w<kBf16, kEpi, 128, 128, D>), dim3(rem << 2), dim3(256), 0, st,
+                           (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias,
+                           (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tiles_m, tiles_n, kGroupM, bulk, 2,
+                           residual_args(g), nullptr, 1);
     } else {
-      auto kern = fp8_gemm_4w<kBf16, kEpi, 256, 128, D>;
-      hipLaunchKernelGGL(kern, dim3(rem << 1), dim3(256), 0, st, (const uint8_t*)g.A, (const uint8_t*)g.W,
-                         g.scales_a, g.scales_b, (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N, g.K, g.ldc,
-                         tiles_m, tiles_n, kGroupM, bulk, 1, residual_args(g), nullptr, 1);
+      if (g.K % 128 == 0)
+        hipLaunchKernelGGL((fp8_gemm_4h<kBf16, kEpi, 256, 128, 3>), dim3(rem << 1), dim3(256), 0, st,
+                           (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias,
+                           (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tiles_m, tiles_n, kGroupM, bulk, 1, residual_args(g));
+      else
+        hipLaunchKernelGGL((fp8_gemm_4w<kBf16, kEpi, 256, 128, D>), dim3(rem << 1), dim3(256), 0, st,
+                           (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias,
+                           (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tiles_m, tiles_n, kGroupM, bulk, 1,
+                           residual_args(g), nullptr, 1);
     }
   }
   return hipGetLastError();
@@ -1376,8 +1502,18 @@ hipError_t launch_gemm_t(const GemmArgs& g, hipStream_t st) {
     const int64_t t128 = (int64_t)((g.M + 127) / 128) * ((g.N + 127) / 128);
     const int64_t t128x256 = (int64_t)((g.M + 127) / 128) * ((g.N + 255) / 256);
     const int64_t t256x192 = (int64_t)((g.M + 255) / 256) * ((g.N + 191) / 192);
+    const int64_t t256x128 = (int64_t)((g.M + 255) / 256) * ((g.N + 127) / 128);
     if (t256 < P) {
       if (t128 <= P) return launch_deepk<kBf16, kEpi, 128, 128, 128, 3, 3>(g, 1, nullptr, st);
+      // 256x128 tiles with 128-byte steps where they fill more CUs than 128x256 (1560 rows: 224
+      // tiles against 208; 1560 x 4096 -> 4096 32.3 us vs 34.0, 1560 x 16384 -> 4096 109.7 vs 112.3)
+      if (t256x128 <= P && t256x128 > t128x256) {
+        const int tm = (g.M + 255) / 256, tn = (g.N + 127) / 128;
+        hipLaunchKernelGGL((fp8_gemm_4h<kBf16, kEpi, 256, 128, 3>), dim3(tm * tn), dim3(256), 0, st,
+                           (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias,
+                           (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tm, tn, 1, 0, -2, residual_args(g));
+        return hipGetLastError();
+      }
       if (t128x256 <= P) return launch_deepk<kBf16, kEpi, 128, 256, 128, 2, 3>(g, 1, nullptr, st);
       if (t256x192 <= P) return launch_direct<kBf16, kEpi, 256, 192, 5>(g, st);
       if (g.K >= 8192) return launch_deepk<kBf16, kEpi, 128, 256, 128, 2, 3>(g, 1, nullptr, st);

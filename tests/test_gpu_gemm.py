@@ -109,13 +109,15 @@ def test_fp16_output_with_denormal_bias(M, N, K):
     assert np.array_equal(y, exp_bits), f"{np.count_nonzero(y != exp_bits)} outputs differ"
 
 
+@pytest.mark.parametrize("K", [128, 192])
 @pytest.mark.parametrize("M,N", [(4352, 4096), (5376, 4096)])
-def test_exact_full_rounds_plus_split_tail(M, N):
+def test_exact_full_rounds_plus_split_tail(M, N, K):
     """More 256x256 tiles than CUs: full rounds run as 256x256 tiles and the last,
     partial round as sub-tiles (on 256 CUs: 272 tiles -> 16 tiles in 4 sub-tiles each;
-    336 tiles -> 80 tiles in 2 sub-tiles each). Exact arithmetic fixes every bit."""
-    announce("gemm exact split tail", M, N)
-    K = 128
+    336 tiles -> 80 tiles in 2 sub-tiles each). The sub-tiles take 128-byte K steps
+    when K % 128 == 0 (K 128: one step) and 64-byte steps otherwise (K 192). Exact
+    arithmetic fixes every bit."""
+    announce("gemm exact split tail", M, N, K)
     rng = np.random.default_rng(M + N)
     qa = f32_to_e4m3fn(rng.integers(-8, 9, (M, K)).astype(np.float32))
     qw = f32_to_e4m3fn(rng.integers(-8, 9, (N, K)).astype(np.float32))
