@@ -720,12 +720,14 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4p(
 #pragma unroll
     for (int i = 0; i < IA; ++i) {
       const int row = (wave * IA + i) * RPL + lrow;
-      oa[i] = (uint32_t)(min(mm + row, M - 1) * K + (lchunk ^ swz_rows<KS>(row)) * 16);
+      // rows past M fall outside the descriptor's range and load zeros (not stored; zero operands
+      // also draw less power than copies of the last row)
+      oa[i] = (uint32_t)(mm + row) * (uint32_t)K + (uint32_t)((lchunk ^ swz_rows<KS>(row)) * 16);
     }
 #pragma unroll
     for (int i = 0; i < IW; ++i) {
       const int row = (wave * IW + i) * RPL + lrow;
-      ow[i] = (uint32_t)(min(nn + row, N - 1) * K + (lchunk ^ swz_rows<KS>(row)) * 16);
+      ow[i] = (uint32_t)(nn + row) * (uint32_t)K + (uint32_t)((lchunk ^ swz_rows<KS>(row)) * 16);
     }
   };
   set_rows(m0, n0);
@@ -964,7 +966,7 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4h(
   constexpr int A_BYTES = BM * KS, SLOT = (BM + BN) * KS;
   constexpr int NMFMA = FM * FN, NREAD = 2 * (FM + FN);
   static_assert(IA * RPL * NW == BM && IW * RPL * NW == BN, "tile rows must split over waves");
-  static_assert(S >= 3 && (S - 1) * LOADS < 64, "vmcnt range");
+  static_assert(S >= 2 && (S - 1) * LOADS < 64, "vmcnt range");
   constexpr int STAGE_BYTES = WTM * (WTN * 2 + 16);
   constexpr int LDS_BYTES = S * SLOT > NW * STAGE_BYTES ? S * SLOT : NW * STAGE_BYTES;
   static_assert(LDS_BYTES <= 160 * 1024, "LDS of one CU");
@@ -1515,7 +1517,13 @@ hipError_t launch_gemm_t(const GemmArgs& g, hipStream_t st) {
         return hipGetLastError();
       }
       if (t128x256 <= P) return launch_deepk<kBf16, kEpi, 128, 256, 128, 2, 3>(g, 1, nullptr, st);
-      if (t256x192 <= P) return launch_direct<kBf16, kEpi, 256, 192, 5>(g, st);
+      if (t256x192 <= P) {  // 1024 x 4096 -> 12288: 48.9 us vs 52.8 with 64-byte steps
+        const int tm = (g.M + 255) / 256, tn = (g.N + 191) / 192;
+        hipLaunchKernelGGL((fp8_gemm_4h<kBf16, kEpi, 256, 192, 2>), dim3(tm * tn), dim3(256), 0, st,
+                           (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias,
+                           (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tm, tn, 1, 0, -2, residual_args(g));
+        return hipGetLastError();
+      }
       if (g.K >= 8192) return launch_deepk<kBf16, kEpi, 128, 256, 128, 2, 3>(g, 1, nullptr, st);
     }
   }
