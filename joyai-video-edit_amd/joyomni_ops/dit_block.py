@@ -32,6 +32,11 @@ per stream (video "img", condition "txt"), with ``mod = table + vec`` split into
   FFN-down FP8 GEMM with the gated residual in its epilogue, in place on the
   stream (``dit.py:508-513,529-538``).
 
+The condition stream runs on a second HIP stream (default priority) between the points
+where the two streams meet -- its QKV and pack beside the video QKV, norm/RoPE and
+cached pack; its projection and FFN beside the video FFN -- joined before attention and
+before returning; the results are those of the serial chain, bit for bit.
+
 Activation quantiser rounding per K follows the reference's ROCm path
 (``fp8_linear.py:57-74``): reciprocal-multiply below K = 8192, division above.
 Weights are random-initialised with the benchmark distributions (there are no
@@ -135,10 +140,15 @@ class QuantizedDoubleStreamBlock:
     """The quantised chain of one two-stream MMDiT block (see the module docstring)."""
 
     def __init__(self, hidden: int, heads: int, mlp_hidden: int, device, generator: torch.Generator,
-                 quant_rounding: str = "reference_rocm"):
+                 quant_rounding: str = "reference_rocm", overlap_streams: bool = True):
         self.hidden, self.heads, self.mlp_hidden = hidden, heads, mlp_hidden
         self.head_dim = hidden // heads
         self.quant_rounding = quant_rounding
+        # the condition stream's kernels run on a second (default-priority) HIP stream, beside the
+        # video stream's, between the points where the two streams meet (joint attention operands,
+        # attention output); results do not depend on it
+        self.overlap_streams = overlap_streams
+        self._side = {}
         self.img = random_stream_weights(hidden, heads, mlp_hidden, generator, device)
         self.txt = random_stream_weights(hidden, heads, mlp_hidden, generator, device)
         for w in (self.img, self.txt):
@@ -204,6 +214,12 @@ class QuantizedDoubleStreamBlock:
             elif c.cos is not None or c.sin is not None:
                 raise ValueError(f"cached slot {c.slot} holds rotated K; it takes no RoPE tables")
 
+    def _side_stream(self, device) -> torch.cuda.Stream:
+        key = torch.device(device).index
+        if key not in self._side:
+            self._side[key] = torch.cuda.Stream(device=device)
+        return self._side[key]
+
     # -- forward ------------------------------------------------------------
     def _cached_into(self, ring: KVRing, cached: Sequence[CachedChunk], k: torch.Tensor, v: torch.Tensor) -> None:
         """Cached chunks into the head of the joint K / V: runs of pre-RoPE slots rotated on read, two
@@ -255,29 +271,59 @@ class QuantizedDoubleStreamBlock:
         img2, txt2 = img.reshape(L, E), txt.reshape(T, E)
         im = self.modulation(self.img, vec)
 
-        # QKV projections
-        q8, s8 = self.norm_quant(img2, im[0], im[1], E)
-        img_qkv = self.img.qkv.gemm(q8, s8)
         if kv_cache_write_only:
             # only the ring is written: Q is not read, no attention operand is produced
+            q8, s8 = self.norm_quant(img2, im[0], im[1], E)
+            img_qkv = self.img.qkv.gemm(q8, s8)
             fused_qkv_norm_rope_cache(img_qkv, H, NORM_EPS, self.img.q_norm, self.img.k_norm, img_cos, img_sin,
                                       None, None, ring_k, ring_v, slot, 0, cache_tokens=n_cache,
                                       cache_pre_rope=kv_cache_pre_rope)
             ring.lengths[write_slot], ring.pre_rope[write_slot] = n_cache, kv_cache_pre_rope
             mark("qkv_norm_rope")
             return img, txt
-        if not skip_text_stream:
-            tm = self.modulation(self.txt, vec)
-            q8, s8 = self.norm_quant(txt2, tm[0], tm[1], E)
-            txt_qkv = self.txt.qkv.gemm(q8, s8)
-        mark("qkv")
 
+        text = not skip_text_stream
         # joint attention operands: Q = [video | condition], K, V = [cached | video | condition]
         C = sum(ring.lengths[c.slot] for c in cached) if cached else 0
         n_q = L if skip_text_stream else L + T
         q = torch.empty(1, n_q, H, D, dtype=torch.bfloat16, device=img.device)
         k = torch.empty(1, C + n_q, H, D, dtype=torch.bfloat16, device=img.device)
         v = torch.empty_like(k)
+        main = torch.cuda.current_stream(img.device)
+        side = self._side_stream(img.device) if text and self.overlap_streams else None
+
+        def text_qkv():
+            tm = self.modulation(self.txt, vec)
+            q8, s8 = self.norm_quant(txt2, tm[0], tm[1], E)
+            return tm, self.txt.qkv.gemm(q8, s8)
+
+        def text_pack(txt_qkv):
+            # condition stream: two-rounding q/k RMSNorm into the tails of Q / K / V
+            tv = txt_qkv.view(1, T, 3, H, D)
+            fused_text_qkv_pack(tv[:, :, 0], tv[:, :, 1], tv[:, :, 2], self.txt.q_norm, self.txt.k_norm, NORM_EPS,
+                                q[:, L:], k[:, C + L:], v[:, C + L:])
+
+        def proj_ffn(x2d, w, m, a, then=None):
+            x = w.proj.gated_residual(a, x2d, m[2])            # new tensor: the caller's input stays
+            if then is not None:
+                then()
+            q8, s8 = self.norm_quant(x, m[3], m[4], E)
+            h = w.up.gemm(q8, s8)
+            w.down.gated_residual(h, x, m[5], inplace=True)
+            return x
+
+        if side is not None:  # fork: the condition stream's QKV and pack beside the video stream's
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                tm, txt_qkv = text_qkv()
+                text_pack(txt_qkv)
+
+        # QKV projections
+        q8, s8 = self.norm_quant(img2, im[0], im[1], E)
+        img_qkv = self.img.qkv.gemm(q8, s8)
+        if text and side is None:
+            tm, txt_qkv = text_qkv()
+        mark("qkv")
 
         # video q/k norm + RoPE into the joint buffers, K / V into the ring
         fused_qkv_norm_rope_cache(img_qkv, H, NORM_EPS, self.img.q_norm, self.img.k_norm, img_cos, img_sin,
@@ -290,25 +336,33 @@ class QuantizedDoubleStreamBlock:
         self._cached_into(ring, cached, k, v)
         mark("cached_kv")
 
-        if not skip_text_stream:
-            # condition stream: two-rounding q/k RMSNorm into the tails of Q / K / V
-            tv = txt_qkv.view(1, T, 3, H, D)
-            fused_text_qkv_pack(tv[:, :, 0], tv[:, :, 1], tv[:, :, 2], self.txt.q_norm, self.txt.k_norm, NORM_EPS,
-                                q[:, L:], k[:, C + L:], v[:, C + L:])
+        if side is not None:
+            main.wait_stream(side)  # join: the condition rows of Q / K / V are written
+        elif text:
+            text_pack(txt_qkv)
         mark("joint_pack")
         attn = self.attention(q, k, v).flatten(2, 3)
         mark("attention")
 
-        streams = [(img2, self.img, im, attn[0, :L])]
-        if not skip_text_stream:
-            streams.append((txt2, self.txt, tm, attn[0, L:]))
-        outs = []
-        for x2d, w, m, a in streams:
-            x = w.proj.gated_residual(a, x2d, m[2])            # new tensor: the caller's input stays
-            q8, s8 = self.norm_quant(x, m[3], m[4], E)
-            h = w.up.gemm(q8, s8)
-            w.down.gated_residual(h, x, m[5], inplace=True)
-            outs.append(x)
+        txt_out = []
+
+        def fork_post():
+            # fork after the video out-projection is queued: the condition stream's projection and
+            # FFN then fill the CUs that the video GEMMs' last partial rounds and the memory-bound
+            # quantisers leave idle (forked right after attention they compete with the video
+            # out-projection's full rounds: 10.25-10.32 vs 10.23-10.29 ms per cfg-4 block, both
+            # streams serial 10.39-10.43)
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                txt_out.append(proj_ffn(txt2, self.txt, tm, attn[0, L:]))
+
+        img_x = proj_ffn(img2, self.img, im, attn[0, :L], fork_post if side is not None else None)
+        txt_x = txt_out[0] if txt_out else None
+        if side is not None:
+            main.wait_stream(side)
+            txt_x.record_stream(main)  # allocated on the side stream, handed to the caller's
+        elif text:
+            txt_x = proj_ffn(txt2, self.txt, tm, attn[0, L:])
         mark("proj_ffn")
-        txt_out = txt if skip_text_stream else outs[1].reshape(1, T, E)
-        return outs[0].reshape(1, L, E), txt_out
+        txt_out = txt if skip_text_stream else txt_x.reshape(1, T, E)
+        return img_x.reshape(1, L, E), txt_out

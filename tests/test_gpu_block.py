@@ -200,6 +200,45 @@ def test_block_chain_full_size_cfg4():
     _full_block_check(5120, 40, 13824, 512, cos_h, sin_h, cached, 404)
 
 
+def test_block_overlapped_streams_match_serial():
+    """The condition stream on its own HIP stream (the default) gives the same bits as the serial
+    chain at the cfg-4 workload: outputs of both streams and the written ring slot, for serial
+    calls and for three overlapped calls queued back to back without a host synchronisation (the
+    second stream's buffers are reused across the queued blocks)."""
+    from joyomni_ops.dit_block import CachedChunk, KVRing, QuantizedDoubleStreamBlock
+    announce("block overlapped streams vs serial")
+    E, H, FFN, T, hh, ww = 5120, 40, 13824, 512, 45, 80
+    L, D = 3 * hh * ww, E // H
+    g = gen(606)
+    blk = QuantizedDoubleStreamBlock(E, H, FFN, DEV, g)
+    img = torch.randn(1, L, E, generator=g).to(torch.bfloat16).to(DEV)
+    txt = torch.randn(1, T, E, generator=g).to(torch.bfloat16).to(DEV)
+    vec = torch.randn(1, E, generator=g).to(torch.bfloat16).to(DEV)
+    cos_h, sin_h = (t.to(DEV) for t in _half_tables([6, 7, 8], hh, ww))
+    cf, sf = (t.to(DEV) for t in _full_tables(list(range(6)), hh, ww))
+    ring = KVRing(4, L, H, D, DEV)
+    cached = []
+    for c, slot in enumerate((2, 3)):
+        ring.k[slot].copy_(torch.randn(L, H, D, generator=g).to(torch.bfloat16))
+        ring.v[slot].copy_(torch.randn(L, H, D, generator=g).to(torch.bfloat16))
+        ring.lengths[slot] = L
+        cached.append(CachedChunk(slot, cf[c * L:(c + 1) * L], sf[c * L:(c + 1) * L]))
+
+    def run():
+        oi, ot = blk.forward(img, txt, vec, cos_h, sin_h, ring=ring, write_slot=0, cached=cached)
+        return [t.clone().view(torch.int16) for t in (oi, ot, ring.k[0], ring.v[0])]
+
+    blk.overlap_streams = False
+    ref = run()
+    torch.cuda.synchronize()
+    blk.overlap_streams = True
+    got = [run() for _ in range(3)]
+    torch.cuda.synchronize()
+    for i, outs in enumerate(got):
+        for name, a, b in zip(("img", "txt", "ring k", "ring v"), outs, ref):
+            assert torch.equal(a, b), f"overlapped call {i}: {name} differs from the serial chain"
+
+
 def test_block_chain_reference_production_geometry():
     """The reference's production block at 480x832: hidden 4096, 32 x 128 heads, FFN 16384; the
     visual sequence is one latent frame of the current chunk plus one reference-video frame
