@@ -514,20 +514,30 @@ def bench_block(steps, warmup, n_cached=2):
         run(False)
     torch.cuda.synchronize()
     acc = {k: 0.0 for k in stages}
+    lat = 0.0
     for _ in range(steps):
         ev = {k: torch.cuda.Event(enable_timing=True) for k in ["start"] + stages}
-        # the timed block is queued behind two untimed ones, as consecutive blocks of a forward
-        # run: its stages start on a busy device (settled clock, no host launch gaps inside it)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        # each timed block is queued behind two untimed ones, as consecutive blocks of a forward
+        # run: its stages start on a busy device (settled clock, no host launch gaps inside it).
+        # The latency comes from a block bracketed by two events only: every event recorded
+        # between kernels leaves the device idle for ~5.5 us (kernel trace), so the block with
+        # the per-stage events gives the stage split, not the latency.
         run(False)
         run(False)
         run(True)
+        run(False)
+        e0.record(stream)
+        run(False)
+        e1.record(stream)
         torch.cuda.synchronize()
+        lat += e0.elapsed_time(e1)
         prev = "start"
         for k in stages:
             acc[k] += ev[prev].elapsed_time(ev[k])
             prev = k
     per = {k: v / steps for k, v in acc.items()}
-    total = sum(per.values())
+    total = lat / steps
     gemm_flops = 0
     for M in (L_TOK, T_COND):
         gemm_flops += 2 * M * (E * 3 * E + E * E + E * FFN + FFN * E)
@@ -535,6 +545,7 @@ def bench_block(steps, warmup, n_cached=2):
                         f"{HEADS}x{HEAD_DIM} heads, FFN {FFN}, {n_cached} cached chunks of {L_TOK} tokens",
             "block_latency_ms": total, "attention_ms": per["attention"],
             "kernel_ms_excl_attention": total - per["attention"], "stages_ms": per,
+            "stages_sum_ms": sum(per.values()),
             "gemm_stage_tflops": gemm_flops / ((per["qkv"] + per["proj_ffn"]) / 1e3) / 1e12,
             "attention_kv_tokens": n_cached * L_TOK + L_TOK + T_COND}
 
