@@ -105,6 +105,13 @@ class KVRing:
         self.lengths = [0] * slots
         # per slot: K stored before RoPE (kv_cache_pre_rope=True) or rotated (the reference's default)
         self.pre_rope = [True] * slots
+        # per slot: bumped on every write through the block (kernels write through raw pointers,
+        # which torch's version counters do not see); in-place torch ops bump ``k._version``
+        self.generation = [0] * slots
+
+    def touch(self, slot: int) -> None:
+        """Record that ``slot`` was rewritten outside torch's view (e.g. by a kernel)."""
+        self.generation[slot] += 1
 
     def key(self, slot: int) -> torch.Tensor:
         return self.k[slot, : self.lengths[slot]][None]
@@ -122,6 +129,39 @@ class CachedChunk:
     slot: int
     cos: Optional[torch.Tensor] = None
     sin: Optional[torch.Tensor] = None
+
+
+@dataclass
+class JointKV:
+    """One layer's joint attention K / V buffers ``[1, cached + video + condition, H, D]`` kept
+    across calls: the cached rows (chunks read from the ring, rotated on read) are assembled on
+    the first call and reused while the cached chunks are unchanged (same ring slots, lengths,
+    storage mode, slot generations, ring version and RoPE tables). The reference memoises the
+    same assembly across the denoising steps of a chunk (``dit.py:1168-1217``,
+    ``_assemble_layer_kv_cache_cached`` ``dit.py:801-816``) and copies it into the joint
+    buffers on every call (``fused_joint_qkv_pack``, ``dit.py:489-496``); here the rows stay
+    where the attention reads them and only the video and condition rows are rewritten."""
+    k: Optional[torch.Tensor] = None
+    v: Optional[torch.Tensor] = None
+    stamp: Optional[tuple] = None
+
+    def invalidate(self) -> None:
+        self.stamp = None
+
+
+def _tensor_key(t: Optional[torch.Tensor]):
+    if t is None:
+        return None
+    return (t.data_ptr(), tuple(t.shape), tuple(t.stride()), str(t.dtype), t._version)
+
+
+def cached_rows_stamp(ring: Optional[KVRing], cached: Sequence[CachedChunk]) -> tuple:
+    """Everything the assembled cached rows depend on; equal stamps mean equal rows."""
+    if not cached:
+        return ()
+    return (id(ring), ring.k.data_ptr(), ring.k._version, ring.v._version,
+            tuple((c.slot, ring.lengths[c.slot], ring.pre_rope[c.slot], ring.generation[c.slot],
+                   _tensor_key(c.cos), _tensor_key(c.sin)) for c in cached))
 
 
 def _adjacent_rows(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
@@ -248,8 +288,8 @@ class QuantizedDoubleStreamBlock:
                 img_sin: torch.Tensor, ring: Optional[KVRing] = None, write_slot: Optional[int] = None,
                 cached: Sequence[CachedChunk] = (), mark: Optional[Callable[[str], None]] = None,
                 skip_text_stream: bool = False, kv_cache_write_only: bool = False,
-                kv_cache_write_seq_len: Optional[int] = None, kv_cache_pre_rope: bool = True
-                ) -> Tuple[torch.Tensor, torch.Tensor]:
+                kv_cache_write_seq_len: Optional[int] = None, kv_cache_pre_rope: bool = True,
+                joint: Optional[JointKV] = None) -> Tuple[torch.Tensor, torch.Tensor]:
         """img [1, L, E], txt [1, T, E], vec [1, E] bf16; img_cos/img_sin bf16 half tables [L, D/2].
 
         Writes the first ``kv_cache_write_seq_len`` (default all) video tokens' K and V into ``ring``
@@ -257,8 +297,9 @@ class QuantizedDoubleStreamBlock:
         attends to [cached chunks | video | condition] (``dit.py:489-498``), or to [cached chunks |
         video] with ``skip_text_stream`` (``dit.py:481-487``; txt is returned unchanged).
         ``kv_cache_write_only`` returns (img, txt) unchanged right after the ring write
-        (``dit.py:446-459``). ``mark(name)`` is called after each stage (the benchmark places timing
-        events there). Returns the updated (img, txt).
+        (``dit.py:446-459``). ``joint`` keeps the joint K / V buffers across calls and reuses their
+        cached rows while the cached chunks are unchanged (``JointKV``). ``mark(name)`` is called after
+        each stage (the benchmark places timing events there). Returns the updated (img, txt).
         """
         mark = mark or (lambda name: None)
         E, H, D = self.hidden, self.heads, self.head_dim
@@ -279,6 +320,7 @@ class QuantizedDoubleStreamBlock:
                                       None, None, ring_k, ring_v, slot, 0, cache_tokens=n_cache,
                                       cache_pre_rope=kv_cache_pre_rope)
             ring.lengths[write_slot], ring.pre_rope[write_slot] = n_cache, kv_cache_pre_rope
+            ring.touch(write_slot)
             mark("qkv_norm_rope")
             return img, txt
 
@@ -287,8 +329,19 @@ class QuantizedDoubleStreamBlock:
         C = sum(ring.lengths[c.slot] for c in cached) if cached else 0
         n_q = L if skip_text_stream else L + T
         q = torch.empty(1, n_q, H, D, dtype=torch.bfloat16, device=img.device)
-        k = torch.empty(1, C + n_q, H, D, dtype=torch.bfloat16, device=img.device)
-        v = torch.empty_like(k)
+        reuse_cached = False
+        if joint is None:
+            k = torch.empty(1, C + n_q, H, D, dtype=torch.bfloat16, device=img.device)
+            v = torch.empty_like(k)
+        else:
+            if joint.k is None or tuple(joint.k.shape) != (1, C + n_q, H, D) or joint.k.device != img.device:
+                joint.k = torch.empty(1, C + n_q, H, D, dtype=torch.bfloat16, device=img.device)
+                joint.v = torch.empty_like(joint.k)
+                joint.stamp = None
+            k, v = joint.k, joint.v
+            stamp = cached_rows_stamp(ring, cached)
+            reuse_cached = joint.stamp == stamp
+            joint.stamp = stamp
         main = torch.cuda.current_stream(img.device)
         side = self._side_stream(img.device) if text and self.overlap_streams else None
 
@@ -331,9 +384,11 @@ class QuantizedDoubleStreamBlock:
                                   cache_tokens=n_cache, cache_pre_rope=kv_cache_pre_rope)
         if write_slot is not None:
             ring.lengths[write_slot], ring.pre_rope[write_slot] = n_cache, kv_cache_pre_rope
+            ring.touch(write_slot)
         mark("qkv_norm_rope")
 
-        self._cached_into(ring, cached, k, v)
+        if not reuse_cached:
+            self._cached_into(ring, cached, k, v)
         mark("cached_kv")
 
         if side is not None:

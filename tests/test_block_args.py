@@ -84,3 +84,40 @@ def test_adjacent_cached_tables_are_joined_without_a_copy():
     assert torch.equal(c, full)
     gap = _adjacent_rows(full[:4], full[5:])
     assert torch.equal(gap, torch.cat([full[:4], full[5:]]))
+
+
+def test_cached_rows_stamp_tracks_every_input_of_the_assembly():
+    """JointKV reuses the assembled cached rows only while this stamp is unchanged: it must move
+    with a write to a cached slot (through torch or through the block), the slot's length or
+    storage mode, a different or modified table, and a different ring; and stay put otherwise."""
+    from joyomni_ops.dit_block import cached_rows_stamp
+    r = _ring()
+    c0, s0 = _tables(16)
+    c1, s1 = _tables(32)
+    cached = [CachedChunk(0, c0, s0), CachedChunk(1, c1, s1)]
+    base = cached_rows_stamp(r, cached)
+    assert cached_rows_stamp(r, cached) == base
+    assert cached_rows_stamp(r, []) == ()
+    r.touch(2)                                   # a slot that is not read
+    assert cached_rows_stamp(r, cached) == base
+    changes = []
+    r.k[1, 0].add_(1.0)                          # in-place write through a view of the ring
+    changes.append(cached_rows_stamp(r, cached))
+    r.v[0, 3].mul_(2.0)
+    changes.append(cached_rows_stamp(r, cached))
+    r.touch(1)                                   # a kernel rewrote a read slot
+    changes.append(cached_rows_stamp(r, cached))
+    r.lengths[0] = 15
+    changes.append(cached_rows_stamp(r, [CachedChunk(0, *_tables(15)), cached[1]]))
+    r.lengths[0] = 16
+    r.pre_rope[1] = False
+    changes.append(cached_rows_stamp(r, cached))
+    r.pre_rope[1] = True
+    c1.add_(0.5)                                 # a table modified in place
+    changes.append(cached_rows_stamp(r, cached))
+    changes.append(cached_rows_stamp(r, [cached[0], CachedChunk(1, c1.clone(), s1)]))  # another tensor
+    changes.append(cached_rows_stamp(_ring(), cached))                                   # another ring
+    seen = [base]
+    for st in changes:
+        assert st not in seen, st
+        seen.append(st)

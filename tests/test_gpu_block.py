@@ -264,6 +264,48 @@ def _small_block(seed, E=512, H=4, FFN=1536, hh=12, ww=20, T=32):
     return g, blk, img, txt, vec
 
 
+def test_block_joint_kv_reuses_cached_rows():
+    """JointKV keeps the joint K / V across calls: a call that reuses the assembled cached rows
+    gives the same bits as one that assembles them; a cached slot changed in place, or rewritten
+    by a block call (as by a later chunk), is assembled again."""
+    from joyomni_ops.dit_block import CachedChunk, JointKV, KVRing
+    announce("block joint K/V reuse")
+    g, blk, img, txt, vec = _small_block(77)
+    L, H, D = img.shape[1], 4, 128
+    cos_h, sin_h = (t.to(DEV) for t in _half_tables([2], 12, 20))
+    cf, sf = (t.to(DEV) for t in _full_tables([0, 1], 12, 20))
+    ring = KVRing(4, L, H, D, DEV)
+    for slot in (2, 3):
+        ring.k[slot].copy_(torch.randn(L, H, D, generator=g).to(torch.bfloat16))
+        ring.v[slot].copy_(torch.randn(L, H, D, generator=g).to(torch.bfloat16))
+        ring.lengths[slot] = L
+    cached = [CachedChunk(2, cf[:L], sf[:L]), CachedChunk(3, cf[L:], sf[L:])]
+    img_d, txt_d, vec_d = img.to(DEV), txt.to(DEV), vec.to(DEV)
+
+    def fwd(joint=None, write_slot=0, cached_=cached):
+        oi, ot = blk.forward(img_d, txt_d, vec_d, cos_h, sin_h, ring=ring, write_slot=write_slot,
+                             cached=cached_, joint=joint)
+        return [t.clone().view(torch.int16) for t in (oi, ot)]
+
+    def same(a, b):
+        return all(torch.equal(x, y) for x, y in zip(a, b))
+
+    joint = JointKV()
+    ref = fwd()
+    assert same(fwd(joint), ref)
+    stamp = joint.stamp
+    assert same(fwd(joint), ref) and joint.stamp == stamp          # cached rows reused
+    ring.v[3].mul_(0.5)                                              # changed in place
+    ref2 = fwd()
+    assert not same(ref2, ref)
+    assert same(fwd(joint), ref2) and joint.stamp != stamp
+    fwd(write_slot=2, cached_=[])                                    # slot 2 rewritten by a block call
+    ref3 = fwd()
+    assert not same(ref3, ref2)
+    assert same(fwd(joint), ref3)
+    assert same(fwd(joint), ref3)
+
+
 @pytest.mark.parametrize("pre_rope", [True, False])
 def test_block_cache_only_forward(pre_rope):
     """kv_cache_write_only (dit.py:446-459): img / txt come back unchanged; the first
