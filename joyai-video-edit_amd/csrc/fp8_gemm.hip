@@ -1417,6 +1417,8 @@ hipError_t launch_deepk(const GemmArgs& g, int splits, float* ws, hipStream_t st
 //   M 256: 128x128 tiles, 128-byte K steps, 3 staging buffers, 3 LDS slots:
 //          N 15360: 35.0 us (41.1) {42.1};  N 5120, 3 splits: 21.6 us (30.4) {28.1}
 //   M 512: N 5120: 128x128 as for M 256: 29.5 us (31.2) {35.7}
+//          (N 15360 / 13824 take 256x128 one-tile-per-workgroup plans before these, in
+//          launch_small_m)
 //          128x256 tiles, 128-byte K steps, 2 staging buffers, 3 LDS slots, where they
 //          fill 3/4 of the CUs or K is long enough to split:
 //          N 15360: 56.7 us (54.6) {62.2};  N 13824: 53.4 us {58.6};
@@ -1456,6 +1458,19 @@ SmallPlan small_plan(int M, int N, int K, bool allow_split) {
 
 template <bool kBf16, int kEpi>
 hipError_t launch_small_m(const GemmArgs& g, hipStream_t st) {
+  if (g.M > 256 && g.K % 128 == 0) {
+    // 257-512 rows where 256x128 tiles fill 3/4 of the CUs: one tile per workgroup with
+    // 128-byte K steps through the DMA ring (M 512 x N 15360: 43-45 us vs 47 for 128x256
+    // deep-K tiles, hipBLASLt 48; x N 13824 with GELU 42 vs 46). With fewer tiles (N 5120)
+    // the deep-K plans stay ahead (128x128 tiles: 30.3 vs 28.8 us).
+    const int tm = (g.M + 255) / 256, tn = (g.N + 127) / 128, P = device_cus();
+    if (4 * tm * tn >= 3 * P && tm * tn <= P) {
+      hipLaunchKernelGGL((fp8_gemm_4h<kBf16, kEpi, 256, 128, 3>), dim3(tm * tn), dim3(256), 0, st,
+                         (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias,
+                         (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tm, tn, 1, 0, -2, residual_args(g));
+      return hipGetLastError();
+    }
+  }
   SmallPlan p = small_plan(g.M, g.N, g.K, true);
   if (p.splits > 1 && (g.workspace == nullptr || g.workspace_bytes < (int64_t)p.splits * g.M * g.N * 4))
     p = small_plan(g.M, g.N, g.K, false);  // no (or too small a) workspace: best plan without a split
