@@ -404,6 +404,20 @@ __device__ __forceinline__ TileJob decode_job(int K, int tiles_m, int tiles_n, i
     const TileCoord tc = map_tile(blockIdx.x, gridDim.x, tiles_n, tiles_m, 1, 0);
     j.m0 = tc.tn * BM;
     j.n0 = tc.tm * BN;
+  } else if (sub_log2 == -4) {
+    // 128x128 sub-tiles of a last round over tiles_m whole 256-row tile rows (the 256x256
+    // tiles from tile_base on, four each), then the top halves of the partial tile row below
+    // them (at most 128 rows remain there), one 128-column block each
+    const int na = (tiles_m * tiles_n - tile_base) << 2;
+    const int w = (int)blockIdx.x;
+    if (w < na) {
+      const TileCoord tc = map_tile(w >> 2, -1, tiles_m, tiles_n, group_m, tile_base);
+      j.m0 = tc.tm * 256 + (w & 1) * 128;
+      j.n0 = tc.tn * 256 + ((w >> 1) & 1) * 128;
+    } else {
+      j.m0 = tiles_m * 256;
+      j.n0 = (w - na) * 128;
+    }
   } else if (sub_log2 < 0) {
     const TileCoord tc = map_tile(blockIdx.x, gridDim.x, tiles_m, tiles_n, group_m, 0);
     j.m0 = tc.tm * 256;
@@ -1251,7 +1265,8 @@ ResidualArgs residual_args(const GemmArgs& g) {
 // not depend on the split (every output element sums its K products in the same order).
 template <bool kBf16, int kEpi>
 hipError_t launch_4w(const GemmArgs& g, hipStream_t st) {
-  const int tiles_m = (g.M + 255) / 256, tiles_n = (g.N + 255) / 256;
+  int tiles_m = (g.M + 255) / 256;
+  const int tiles_n = (g.N + 255) / 256;
   const int T = tiles_m * tiles_n, P = device_cus();
   int rem = T % P;
   int sub_log2 = 0;
@@ -1262,8 +1277,26 @@ hipError_t launch_4w(const GemmArgs& g, hipStream_t st) {
   } else {
     rem = 0;  // the last round is nearly full: no split
   }
+  // With at most 128 rows in the last tile row, its 256x256 tiles are mostly padding: when the
+  // whole tile rows' leftover tiles (as 128x128 quarters) and the last row's top halves (one
+  // 128x128 tile per 128 columns) fit one round, that round takes a quarter tile's time instead
+  // of a half (1560 x 4096 -> 12288: one round of 256 tiles, then 32 x 4 + 96 = 224 quarter tiles
+  // instead of 80 x 2 half tiles)
+  bool last_row_quarters = false;
+  const int m_rows = g.M % 256;
+  if (m_rows > 0 && m_rows <= 128 && g.M > 256 && g.K % 128 == 0) {
+    const int tf = (g.M / 256) * tiles_n;
+    const int lq = (tf % P) * 4 + (g.N + 127) / 128;
+    const int cost_now = 4 * (T / P) + (rem == 0 ? 4 * ((T % P) != 0) : (sub_log2 == 2 ? 1 : 2));
+    if (tf >= P && lq <= P && 4 * (tf / P) + 1 < cost_now) last_row_quarters = true;
+  }
+  if (last_row_quarters) {
+    tiles_m = g.M / 256;
+    rem = (tiles_m * tiles_n) % P;
+    sub_log2 = -4;
+  }
   constexpr int D = 5;  // DMA ring depth
-  const int bulk = T - rem;
+  const int bulk = tiles_m * tiles_n - rem;
   // the persistent kernel takes the full rounds (or a single partial one) when its layout
   // rules hold (K steps in pairs of 128 bytes, row scales read 4 at a time, 32-bit buffer
   // offsets, a workgroup count that keeps the XCD mapping); with fewer tiles than CUs it
@@ -1286,7 +1319,12 @@ hipError_t launch_4w(const GemmArgs& g, hipStream_t st) {
                        g.scales_b, (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tiles_m, tiles_n,
                        kGroupM, 0, -1, residual_args(g), nullptr, 1);
   }
-  if (rem > 0) {
+  if (last_row_quarters) {
+    const int nq = rem * 4 + (g.N + 127) / 128;
+    hipLaunchKernelGGL((fp8_gemm_4h<kBf16, kEpi, 128, 128, 4>), dim3(nq), dim3(256), 0, st, (const uint8_t*)g.A,
+                       (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N,
+                       g.K, g.ldc, tiles_m, tiles_n, kGroupM, bulk, -4, residual_args(g));
+  } else if (rem > 0) {
     if (sub_log2 == 2) {
       if (g.K % 128 == 0)
         hipLaunchKernelGGL((fp8_gemm_4h<kBf16, kEpi, 128, 128, 4>), dim3(rem << 2), dim3(256), 0, st,

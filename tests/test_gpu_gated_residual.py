@@ -85,7 +85,8 @@ def test_exact_fp16():
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("M,N,K", [(64, 5120, 5120), (256, 15360, 1024), (400, 15360, 640), (4352, 4352, 256),
+@pytest.mark.parametrize("M,N,K", [(64, 5120, 5120), (256, 15360, 1024), (400, 15360, 640), (1560, 12288, 256),
+                                   (4352, 4352, 256),
                                    (2048, 5120, 13824), (777, 1000, 320),
                                    # persistent 256x256 kernel (K % 256 == 0, M % 4 == 0): a whole
                                    # round plus a sub-tile tail, and a single partial round

@@ -128,6 +128,25 @@ def test_exact_full_rounds_plus_split_tail(M, N, K):
     assert np.array_equal(u16(gemm(qa, qw, sa, sw, bias)), exp_bits)
 
 
+@pytest.mark.parametrize("K", [128, 256])
+def test_exact_last_tile_row_as_quarter_tiles(K):
+    """At most 128 rows in the last 256-row tile row, and one whole round of 256x256 tiles plus
+    leftovers: the leftover tiles as 128x128 quarters and the last row's top halves run as one
+    round of 128x128 sub-tiles (1560 x 12288 on 256 CUs: 256 tiles, then 32 x 4 + 96 = 224
+    sub-tiles). K 256 runs the whole round persistently, K 128 as one tile per workgroup.
+    Exact arithmetic fixes every bit."""
+    M, N = 1560, 12288
+    announce("gemm exact last-row quarter tiles", M, N, K)
+    rng = np.random.default_rng(M + N + K)
+    qa = f32_to_e4m3fn(rng.integers(-8, 9, (M, K)).astype(np.float32))
+    qw = f32_to_e4m3fn(rng.integers(-8, 9, (N, K)).astype(np.float32))
+    sa = (2.0 ** rng.integers(-8, 2, M)).astype(np.float32)
+    sw = (2.0 ** rng.integers(-8, 2, N)).astype(np.float32)
+    bias = f32_to_bf16((rng.integers(-64, 64, N) / 16).astype(np.float32))
+    exp_bits, _ = og.scaled_mm(qa, qw, sa, sw, bias)
+    assert np.array_equal(u16(gemm(qa, qw, sa, sw, bias)), exp_bits)
+
+
 def test_cfg0_single_linear():
     announce("gemm cfg0 256x4096x4096")
     qa, sa, qw, sw, bias = quantized_problem(256, 4096, 4096, 0)
