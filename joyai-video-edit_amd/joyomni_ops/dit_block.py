@@ -341,7 +341,7 @@ class QuantizedDoubleStreamBlock:
             k, v = joint.k, joint.v
             stamp = cached_rows_stamp(ring, cached)
             reuse_cached = joint.stamp == stamp
-            joint.stamp = stamp
+            joint.stamp = None  # set again once the cached rows are assembled
         main = torch.cuda.current_stream(img.device)
         side = self._side_stream(img.device) if text and self.overlap_streams else None
 
@@ -389,6 +389,8 @@ class QuantizedDoubleStreamBlock:
 
         if not reuse_cached:
             self._cached_into(ring, cached, k, v)
+        if joint is not None:
+            joint.stamp = stamp
         mark("cached_kv")
 
         if side is not None:
