@@ -188,7 +188,6 @@ class QuantizedDoubleStreamBlock:
         # video stream's, between the points where the two streams meet (joint attention operands,
         # attention output); results do not depend on it
         self.overlap_streams = overlap_streams
-        self._side = {}
         self.img = random_stream_weights(hidden, heads, mlp_hidden, generator, device)
         self.txt = random_stream_weights(hidden, heads, mlp_hidden, generator, device)
         for w in (self.img, self.txt):
@@ -254,11 +253,15 @@ class QuantizedDoubleStreamBlock:
             elif c.cos is not None or c.sin is not None:
                 raise ValueError(f"cached slot {c.slot} holds rotated K; it takes no RoPE tables")
 
-    def _side_stream(self, device) -> torch.cuda.Stream:
-        key = torch.device(device).index
-        if key not in self._side:
-            self._side[key] = torch.cuda.Stream(device=device)
-        return self._side[key]
+    _side_streams = {}  # one second stream per device, shared by every block
+
+    @classmethod
+    def _side_stream(cls, device) -> torch.cuda.Stream:
+        dev = torch.device(device)
+        key = dev.index if dev.index is not None else torch.cuda.current_device()
+        if key not in cls._side_streams:
+            cls._side_streams[key] = torch.cuda.Stream(device=key)
+        return cls._side_streams[key]
 
     # -- forward ------------------------------------------------------------
     def _cached_into(self, ring: KVRing, cached: Sequence[CachedChunk], k: torch.Tensor, v: torch.Tensor) -> None:
