@@ -313,9 +313,10 @@ def test_small_m_split_random_within_tolerance(M, N, K):
 
 
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("M,N,K", [(200, 520, 512), (64, 2048, 4096), (300, 2560, 5120)])
+@pytest.mark.parametrize("M,N,K", [(200, 520, 512), (64, 2048, 4096), (300, 2560, 5120), (400, 12296, 512)])
 def test_gelu_epilogue_and_fp16_out_plans(out_dtype, M, N, K):
-    """GELU-tanh on the rounded output, on unsplit and split small-M plans."""
+    """GELU-tanh on the rounded output, on unsplit and split small-M plans and the one-tile 256x128
+    plan of 257-512 rows (400 x 12296: 194 tiles, a partial last tile column)."""
     announce("gemm gelu plan", out_dtype, M, N, K)
     qa, sa, qw, sw, bias = quantized_problem(M, N, K, 11 + M)
     bias_t = torch.from_numpy(bf16_to_f32(bias)).to(out_dtype)
