@@ -1146,21 +1146,17 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4k(
   operand_rows<IA, IW, KS>(A, W, M, N, K, job, wave, lane, pa, pw);
 
   v4i stg[U][LOADS];
-  // With a single row of tiles every W byte is read by one workgroup only: non-temporal loads
-  // (M 64 x N 15360: 21.2 -> 20.1 us). With several, workgroups of one XCD share W through L2.
-  const bool w_once = tiles_m == 1;
+  // W with default-policy loads also where a single row of tiles reads every W byte once:
+  // non-temporal loads there were 1.1 us faster with 256-byte steps (M 64 x N 15360), are level
+  // with the 512-byte steps in back-to-back launches (20.0 us), and 3 us slower for a launch that
+  // starts on an idle device (25.9 vs 22.9 us)
   auto gload = [&](auto bc, int kt) {
     constexpr int B = decltype(bc)::value;
     const int64_t koff = (int64_t)min(kt, nk - 1) * KS;
 #pragma unroll
     for (int i = 0; i < IA; ++i) stg[B][i] = *(const v4i*)(pa[i] + koff);
-    if (w_once) {
 #pragma unroll
-      for (int i = 0; i < IW; ++i) stg[B][IA + i] = __builtin_nontemporal_load((const v4i*)(pw[i] + koff));
-    } else {
-#pragma unroll
-      for (int i = 0; i < IW; ++i) stg[B][IA + i] = *(const v4i*)(pw[i] + koff);
-    }
+    for (int i = 0; i < IW; ++i) stg[B][IA + i] = *(const v4i*)(pw[i] + koff);
   };
   auto lwrite = [&](auto bc, int slot) {
     constexpr int B = decltype(bc)::value;
