@@ -144,6 +144,44 @@ def _time_eager(fn, steps: int):
     return start.elapsed_time(end) / 1e3 / steps
 
 
+class TunedReference:
+    """PyTorch TunableOp around a reference torch._scaled_mm leg, with the reference's own settings
+    (deploy/tune_rocm_fp8.py:46-66: tuning on, untuned-GEMM recording off, at most 10 ms and 30
+    iterations per candidate). The first call of each shape inside the context tunes it (the
+    warm-up calls of time_launches, before the graph capture); TunableOp is switched off again on
+    exit, so the untuned legs elsewhere keep hipBLASLt's default selection. The deployment loads
+    the table with tuning off (serve_joyomni_streaming.py:77-102): the same kernels, chosen here
+    in-process instead of from a file."""
+
+    configured = False
+
+    @classmethod
+    def configure(cls, csv=None):
+        from torch.cuda import tunable
+        import tempfile
+        path = csv or os.path.join(tempfile.gettempdir(), f"joy_bench_tunableop_{os.getpid()}.csv")
+        # results go to that file at exit (a temporary one unless --tunableop names one)
+        tunable.set_filename(path, insert_device_ordinal=False)
+        tunable.record_untuned_enable(False)
+        tunable.set_max_tuning_duration(10)
+        tunable.set_max_tuning_iterations(30)
+        cls.configured = True
+
+    def __enter__(self):
+        from torch.cuda import tunable
+        if not TunedReference.configured:
+            TunedReference.configure()
+        tunable.enable(True)
+        tunable.tuning_enable(True)
+        return self
+
+    def __exit__(self, *exc):
+        from torch.cuda import tunable
+        tunable.tuning_enable(False)
+        tunable.enable(False)
+        return False
+
+
 def progress(msg: str) -> None:
     """One line on stderr per finished section, so a long run shows it is alive."""
     print(f"bench: {msg}", file=sys.stderr, flush=True)
@@ -189,7 +227,9 @@ def bench_gemm(steps, warmup):
     for name, K, N in GEMM_SHAPES:
         g = torch.Generator().manual_seed(K + N)
         M = L_TOK
-        x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
+        # benchmark cfg 2 draws its operands like cfg 0: activations N(0,1) with 0.5 % of the
+        # channels scaled x20 (outliers), weights N(0, 0.02)
+        x = outlier_acts(M, K, g).to(dev)
         w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).to(dev)
         bias = (torch.randn(N, generator=g) * 0.01).to(torch.bfloat16).to(dev)
         qa = torch.empty(M, K, dtype=torch.float8_e4m3fn, device=dev)
@@ -219,17 +259,36 @@ def bench_gemm(steps, warmup):
             tr = time_launches(reference_path, steps, warmup)
             rec["reference_hipblaslt_tflops"] = flops / tr / 1e12
             rec["speedup_vs_reference_gpu"] = tr / t
+            with TunedReference():
+                tt = time_launches(reference_path, steps, warmup)
+            rec["reference_hipblaslt_tuned_tflops"] = flops / tt / 1e12
+            rec["speedup_vs_reference_gpu_tuned"] = tt / t
         except Exception as exc:  # pragma: no cover - depends on the torch build
             rec["reference_hipblaslt_tflops"] = None
             rec["reference_hipblaslt_error"] = str(exc)[:200]
         res.append(rec)
+        progress(f"cfg2 {name} {M}x{K}x{N}: {t * 1e6:.1f} us, {rec['tflops']:.0f} TFLOP/s "
+                 f"({rec['frac_fp8_peak']:.3f} of FP8 peak); hipBLASLt {rec.get('reference_hipblaslt_tflops') or 0:.0f}, "
+                 f"tuned {rec.get('reference_hipblaslt_tuned_tflops') or 0:.0f} TFLOP/s")
         del x, w, qa, qw
     tot_flops = sum(2 * r["M"] * r["N"] * r["K"] for r in res)
     tot_t = sum(r["ms"] for r in res) / 1e3
     ref_t = [2 * r["M"] * r["N"] * r["K"] / r["reference_hipblaslt_tflops"] / 1e12
              for r in res if r.get("reference_hipblaslt_tflops")]
     ref_agg = tot_flops / sum(ref_t) / 1e12 if len(ref_t) == len(res) else None
-    return res, tot_flops / tot_t / 1e12, ref_agg
+    tuned_t = [2 * r["M"] * r["N"] * r["K"] / r["reference_hipblaslt_tuned_tflops"] / 1e12
+               for r in res if r.get("reference_hipblaslt_tuned_tflops")]
+    tuned_agg = tot_flops / sum(tuned_t) / 1e12 if len(tuned_t) == len(res) else None
+    return res, tot_flops / tot_t / 1e12, ref_agg, tuned_agg
+
+
+def outlier_acts(M, K, g):
+    """Benchmark cfg 0 activations (also cfg 2's, "same seeded distributions as config 0"):
+    N(0,1) bf16 with 0.5 % of the channels scaled x20."""
+    import torch
+    x = torch.randn(M, K, generator=g)
+    x[:, torch.randperm(K, generator=g)[: K // 200]] *= 20
+    return x.to(torch.bfloat16)
 
 
 def bench_cfg0(steps, warmup):
@@ -331,13 +390,20 @@ def bench_reference_shapes(steps, warmup):
         swr = sw.reshape(1, N)
         t = time_launches(Rotation(weights, lambda q: jo.fp8_scaled_mm(qa, q.t(), sa, swr, torch.bfloat16, bias)),
                           steps, warmup)
-        tr = time_launches(Rotation(weights, lambda q: torch._scaled_mm(
-            qa, q.t(), scale_a=sa, scale_b=swr, bias=bias, out_dtype=torch.bfloat16, use_fast_accum=True)),
-            steps, warmup)
+        def reference_path():
+            return time_launches(Rotation(weights, lambda q: torch._scaled_mm(
+                qa, q.t(), scale_a=sa, scale_b=swr, bias=bias, out_dtype=torch.bfloat16, use_fast_accum=True)),
+                steps, warmup)
+        tr = reference_path()
+        with TunedReference():  # the table the reference deploys for exactly these shapes
+            tt = reference_path()
         flops = 2 * M * N * K
         out.append({"M": M, "K": K, "N": N, "us": t * 1e6, "tflops": flops / t / 1e12,
                     "reference_hipblaslt_us": tr * 1e6, "reference_hipblaslt_tflops": flops / tr / 1e12,
-                    "speedup_vs_reference_gpu": tr / t})
+                    "speedup_vs_reference_gpu": tr / t, "reference_hipblaslt_tuned_us": tt * 1e6,
+                    "speedup_vs_reference_gpu_tuned": tt / t})
+        progress(f"refgemm {M}x{K}x{N}: {t * 1e6:.1f} us; hipBLASLt {tr * 1e6:.1f} us, tuned {tt * 1e6:.1f} us "
+                 f"({tt / t:.3f}x)")
         del weights
     return out
 
@@ -372,9 +438,17 @@ def bench_small_m(steps, warmup):
                 qa, qw.t(), scale_a=sa, scale_b=sw.reshape(1, N), bias=bias, out_dtype=torch.bfloat16,
                 use_fast_accum=True)), steps, warmup)
             b = gemm_bytes(M, N, K)
+            flops = 2 * M * N * K
+            # the binding roof: HBM below the ridge point (625 FLOP/B), the FP8 MFMA peak above it
+            t_roof = max(b / (PEAK_HBM_GBS * 1e9), flops / (PEAK_FP8_TFLOPS * 1e12))
+            bound = "hbm" if b / (PEAK_HBM_GBS * 1e9) >= flops / (PEAK_FP8_TFLOPS * 1e12) else "mfma"
             out.append({"M": M, "K": K, "N": N, "us": t * 1e6, "gbs": b / t / 1e9,
-                        "frac_hbm_peak": b / t / 1e9 / PEAK_HBM_GBS, "weight_copies": len(weights),
+                        "frac_hbm_peak": b / t / 1e9 / PEAK_HBM_GBS, "tflops": flops / t / 1e12,
+                        "flop_per_byte": flops / b, "roofline_bound": bound, "frac_roofline": t_roof / t,
+                        "weight_copies": len(weights),
                         "reference_hipblaslt_us": tr * 1e6, "speedup_vs_reference_gpu": tr / t})
+            progress(f"cfg3 M {M} x N {N}: {t * 1e6:.1f} us ({bound}-bound, {t_roof / t:.3f} of roofline); "
+                     f"hipBLASLt {tr * 1e6:.1f} us")
         del weights
     return out
 
@@ -465,7 +539,7 @@ def bench_norm(steps, warmup):
     return out
 
 
-def bench_block(steps, warmup, n_cached=2):
+def bench_block(steps, warmup, n_cached=2, attention_backend="hip"):
     """Benchmark cfg 4: one two-stream MMDiT block's quantised chain, video 10800 + condition 512
     tokens, hidden 5120, 40 x 128 heads, FFN 13824, random-init weights; the video chunk's K/V go
     into ring slot 0 and the block attends to ``n_cached`` cached chunks of 10800 tokens read from
@@ -481,7 +555,7 @@ def bench_block(steps, warmup, n_cached=2):
     dev = torch.device("cuda:0")
     g = torch.Generator().manual_seed(5)
     T_COND, FFN = 512, 13824
-    blk = QuantizedDoubleStreamBlock(E, HEADS, FFN, dev, g)
+    blk = QuantizedDoubleStreamBlock(E, HEADS, FFN, dev, g, attention_backend=attention_backend)
     img = torch.randn(1, L_TOK, E, generator=g).to(torch.bfloat16).to(dev)
     txt = torch.randn(1, T_COND, E, generator=g).to(torch.bfloat16).to(dev)
     vec = torch.randn(1, E, generator=g).to(torch.bfloat16).to(dev)
@@ -567,7 +641,8 @@ def bench_block(steps, warmup, n_cached=2):
     gemm_flops = 0
     for M in (L_TOK, T_COND):
         gemm_flops += 2 * M * (E * 3 * E + E * E + E * FFN + FFN * E)
-    return {"workload": f"cfg4 block: video {L_TOK} + condition {T_COND} tokens, hidden {E}, "
+    return {"attention_backend": attention_backend,
+            "workload": f"cfg4 block: video {L_TOK} + condition {T_COND} tokens, hidden {E}, "
                         f"{HEADS}x{HEAD_DIM} heads, FFN {FFN}, {n_cached} cached chunks of {L_TOK} tokens "
                         f"(ring write of the chunk every call; cached rows of the joint K / V reused "
                         f"across calls as across denoising steps, or assembled in the call: *_first_step)",
@@ -715,6 +790,56 @@ def cpu_baseline_gemm():
                       "fp32 dequantise-then-matmul + bias -> bf16"}
 
 
+def summary(rec):
+    """Compact digest of the line's sections (rounded figures), printed as its last key."""
+    r = lambda v, n=1: None if v is None else round(v, n)  # noqa: E731
+    out = {}
+    if "roofline" in rec:
+        out["cfg1_qkv_norm_rope"] = {"us": r(rec["ms_per_step"] * 1e3), "gbs": rec["value"],
+                                     "frac_hbm": rec["roofline"]["frac"]}
+    if "gemm_cfg2" in rec:
+        gc = rec["gemm_cfg2"]
+        out["cfg2_gemm"] = {"tflops": gc["aggregate_tflops"], "frac_fp8": gc["roofline"]["frac"],
+                            "hipblaslt": gc["reference_hipblaslt_aggregate_tflops"],
+                            "hipblaslt_tuned": gc["reference_hipblaslt_tuned_aggregate_tflops"],
+                            "shapes_us_tflops_hipblaslt_tuned": {
+                                x["shape"]: [r(x["ms"] * 1e3), r(x["tflops"], 0), r(x.get("reference_hipblaslt_tflops"), 0),
+                                             r(x.get("reference_hipblaslt_tuned_tflops"), 0)] for x in gc["shapes"]}}
+    if "gemm_reference_shapes" in rec:
+        gr = rec["gemm_reference_shapes"]
+        out["refgemm_12"] = {"us": r(gr["total_us"], 0), "hipblaslt_us": r(gr["reference_hipblaslt_total_us"], 0),
+                             "hipblaslt_tuned_us": r(gr["reference_hipblaslt_tuned_total_us"], 0),
+                             "speedup_tuned_per_shape": [r(x["speedup_vs_reference_gpu_tuned"], 3) for x in gr["shapes"]]}
+    if "gemm_cfg3_small_m" in rec:
+        out["cfg3_M_N_us_bound_frac_hipblaslt_us"] = [
+            [x["M"], x["N"], r(x["us"]), x["roofline_bound"], r(x["frac_roofline"], 3), r(x["reference_hipblaslt_us"])]
+            for x in rec["gemm_cfg3_small_m"]]
+    if "cfg0_linear" in rec:
+        out["cfg0_linear_us"] = r(rec["cfg0_linear"]["us"])
+    if "act_quant" in rec:
+        out["act_quant_frac_hbm"] = [r(x["frac_hbm_peak"], 3) for x in rec["act_quant"]]
+    if "adaln_norm" in rec:
+        out["adaln_norm_frac_hbm"] = [r(x["frac_hbm_peak"], 3) for x in rec["adaln_norm"]]
+    if "kv_pack" in rec:
+        out["kv_pack_frac_hbm"] = [r(x["frac_hbm_peak"], 3) for x in rec["kv_pack"]]
+    if "attention_core" in rec:
+        a = rec["attention_core"]
+        out["attention"] = {"ms": r(a["ms"], 2), "frac_bf16": r(a["frac_bf16_peak"], 3),
+                            "torch_sdpa_ms": r(a["reference_sdpa_ms"], 2)}
+    if "block_cfg4" in rec:
+        b = rec["block_cfg4"]
+        out["block_cfg4_ms"] = {"hip_attention": r(b["block_latency_ms"], 2),
+                                "hip_attention_first_step": r(b["block_latency_first_step_ms"], 2),
+                                "attention": r(b["attention_ms"], 2)}
+        if "block_cfg4_torch_sdpa" in rec:
+            bs = rec["block_cfg4_torch_sdpa"]
+            out["block_cfg4_ms"].update({"torch_sdpa_attention": r(bs["block_latency_ms"], 2),
+                                         "torch_sdpa_attention_part": r(bs["attention_ms"], 2)})
+    if "cpu_baseline" in rec:
+        out["cpu_baseline_gbs"] = r(rec["cpu_baseline"]["value"], 2)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -738,14 +863,7 @@ def main():
 
     import torch
     import joyomni_ops  # noqa: F401  (fails loudly if the HIP library is missing)
-    if args.tunableop:
-        from torch.cuda import tunable
-        tunable.set_filename(args.tunableop, insert_device_ordinal=False)
-        tunable.enable(True)
-        tunable.tuning_enable(True)
-        tunable.record_untuned_enable(False)
-        tunable.set_max_tuning_duration(10)
-        tunable.set_max_tuning_iterations(30)
+    TunedReference.configure(args.tunableop)
     props = torch.cuda.get_device_properties(0)
     rec = {"metric": METRIC, "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
@@ -767,10 +885,12 @@ def main():
     if args.only in ("all", "gemm"):
         # all `steps` calls in one graph: a graph replay carries a fixed start-up cost, which a
         # short graph spreads over few calls (and an op of two launches pays about twice)
-        res, agg, ref_agg = bench_gemm(args.steps, max(2, args.warmup // 2))
+        res, agg, ref_agg, tuned_agg = bench_gemm(args.steps, max(2, args.warmup // 2))
         best = max(res, key=lambda r: r["tflops"])
         rec["gemm_cfg2"] = {"shapes": res, "aggregate_tflops": round(agg, 1),
                             "reference_hipblaslt_aggregate_tflops": round(ref_agg, 1) if ref_agg else None,
+                            "reference_hipblaslt_tuned_aggregate_tflops": round(tuned_agg, 1) if tuned_agg else None,
+                            "activations": "cfg 0 distribution: N(0,1) with 0.5 % of channels x20",
                             "roofline": {"bound": "mfma", "achieved": round(agg, 1), "peak": PEAK_FP8_TFLOPS,
                                          "unit": "TFLOP/s", "frac": round(agg / PEAK_FP8_TFLOPS, 4),
                                          "traffic": load_traffic("fp8_gemm_qkv"),
@@ -785,9 +905,13 @@ def main():
         rs = bench_reference_shapes(args.steps, max(2, args.warmup // 2))
         t_ours = sum(r["us"] for r in rs)
         t_ref = sum(r["reference_hipblaslt_us"] for r in rs)
+        t_tuned = sum(r["reference_hipblaslt_tuned_us"] for r in rs)
         rec["gemm_reference_shapes"] = {"shapes": rs, "total_us": t_ours, "reference_hipblaslt_total_us": t_ref,
-                                        "speedup_vs_reference_gpu": t_ref / t_ours}
-        progress(f"reference tuned GEMM shapes: {t_ours:.0f} us vs hipBLASLt {t_ref:.0f} us")
+                                        "speedup_vs_reference_gpu": t_ref / t_ours,
+                                        "reference_hipblaslt_tuned_total_us": t_tuned,
+                                        "speedup_vs_reference_gpu_tuned": t_tuned / t_ours}
+        progress(f"reference tuned GEMM shapes: {t_ours:.0f} us vs hipBLASLt {t_ref:.0f} us untuned, "
+                 f"{t_tuned:.0f} us TunableOp-tuned")
     if args.only in ("all", "small"):
         rec["gemm_cfg3_small_m"] = bench_small_m(args.steps, args.warmup)
         progress("cfg3 small-M GEMMs done")
@@ -808,13 +932,19 @@ def main():
         rec["block_cfg4"] = bench_block(max(3, args.steps // 10), max(1, args.warmup // 5))
         progress(f"cfg4 block {rec['block_cfg4']['block_latency_ms']:.2f} ms "
                  f"(first step on a chunk's cache {rec['block_cfg4']['block_latency_first_step_ms']:.2f} ms)")
+        # BASELINE cfg 4 as stated: the attention core is the reference's F.scaled_dot_product_attention
+        # (dit.py:154-167), inside the block latency
+        rec["block_cfg4_torch_sdpa"] = bench_block(max(3, args.steps // 10), max(1, args.warmup // 5),
+                                                   attention_backend="torch_sdpa")
+        progress(f"cfg4 block with torch SDPA attention {rec['block_cfg4_torch_sdpa']['block_latency_ms']:.2f} ms "
+                 f"(attention {rec['block_cfg4_torch_sdpa']['attention_ms']:.2f} ms)")
     if args.only == "copy":
         rec["copy"] = bench_copy(args.steps, args.warmup)
     if args.only == "clock":
         rec["clock"] = bench_clock(max(args.steps, 13), max(args.warmup, 1))
-    if args.tunableop:
-        from torch.cuda import tunable
-        rec["tunableop"] = {"file": args.tunableop, "tuned_results": len(tunable.get_results())}
+    from torch.cuda import tunable
+    rec["tunableop"] = {"file": args.tunableop, "tuned_results": len(tunable.get_results()),
+                        "settings": "reference deploy/tune_rocm_fp8.py: 10 ms, 30 iterations"}
     if not args.no_cpu:
         if args.only in ("all", "qkv"):
             rec["cpu_baseline"] = cpu_baseline_qkv()
@@ -822,6 +952,7 @@ def main():
             rec["cpu_baseline_gemm"] = cpu_baseline_gemm()
         if args.only == "all":
             rec["cpu_baselines_more"] = cpu_baselines_more()
+    rec["summary"] = summary(rec)  # last key: the part of the line a tail of it keeps
     print(json.dumps(rec), flush=True)
 
 

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define JOY_ABI_VERSION 8
+#define JOY_ABI_VERSION 9
 
 #if defined(__GNUC__) || defined(__clang__)
 #define JOY_API __attribute__((visibility("default")))
@@ -57,6 +57,17 @@ JOY_API int joy_abi_version(void);
 
 /* Message for the last non-OK status returned on the calling thread ("" if none). */
 JOY_API const char *joy_last_error(void);
+
+/*
+ * Optional set-up (no reference counterpart): resolves, for every visible device, the
+ * per-device library state that an entry point otherwise sets up on its first call on
+ * that device -- today the address of joy_fp8_scaled_mm_noalloc's scratch array
+ * (hipGetSymbolAddress, which may load the code object). Call it once per process before
+ * capturing into a HIP graph a joy_fp8_scaled_mm_noalloc call that may be the first on its
+ * device, so that the captured call makes no runtime query. Allocates nothing; leaves the
+ * caller's current device unchanged; returns JOY_OK with no visible device.
+ */
+JOY_API joy_status joy_init(void);
 
 /*
  * Dynamic per-token FP8 quantisation.
@@ -121,6 +132,8 @@ JOY_API int64_t joy_fp8_scaled_mm_workspace_size(int64_t M, int64_t N, int64_t K
  * Problems whose split-K plan needs more scratch than that return
  * JOY_ERR_UNSUPPORTED before anything is launched. Every call on one GPU shares that
  * GPU's scratch: calls that overlap on one GPU (different streams or threads) race.
+ * The scratch address is resolved by joy_init() or, failing that, on the first call on
+ * each device (call joy_init() before capturing such a first call into a HIP graph).
  */
 JOY_API joy_status joy_fp8_scaled_mm_noalloc(const void *mat_a, const void *mat_b, const float *scales_a,
                                              const float *scales_b, const void *bias, void *out, int out_dtype,

@@ -100,18 +100,25 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
 
-joy_status scratch_for_current_device(void** out) {
-  int dev = -1;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return hip_status(e, "hipGetDevice");
+// Address of the scratch array on device `dev`, which must be the current device.
+joy_status resolve_scratch(int dev) {
   if (dev < 0 || dev >= kMaxDevices) return fail(JOY_ERR_UNSUPPORTED, "device %d: at most %d devices", dev, kMaxDevices);
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
     void* p = nullptr;
-    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess) return hip_status(e, "hipGetSymbolAddress(scratch)");
     g_scratch_ptr[dev] = p;
   }
+  return JOY_OK;
+}
+
+joy_status scratch_for_current_device(void** out) {
+  int dev = -1;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e, "hipGetDevice");
+  const joy_status st = resolve_scratch(dev);
+  if (st != JOY_OK) return st;
   *out = g_scratch_ptr[dev];
   return JOY_OK;
 }
@@ -123,6 +130,27 @@ extern "C" {
 int joy_abi_version(void) { return JOY_ABI_VERSION; }
 
 const char* joy_last_error(void) { return g_err; }
+
+joy_status joy_init(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+    (void)hipGetLastError();  // no visible device: nothing to resolve
+    return ok();
+  }
+  int cur = 0;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) return hip_status(e, "hipGetDevice");
+  for (int d = 0; d < n && d < kMaxDevices; ++d) {
+    e = hipSetDevice(d);
+    if (e != hipSuccess) return hip_status(e, "hipSetDevice");
+    const joy_status st = resolve_scratch(d);
+    if (st != JOY_OK) {
+      (void)hipSetDevice(cur);
+      return st;
+    }
+  }
+  return hip_status(hipSetDevice(cur), "hipSetDevice");
+}
 
 joy_status joy_per_token_quant_fp8(const void* input, int input_dtype, void* output_q,
                                    float* output_s, int64_t M, int64_t K, int rounding,

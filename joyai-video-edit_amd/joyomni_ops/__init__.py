@@ -54,10 +54,13 @@ __all__ = [
 _NS = "joyomni_ops"
 _lib_def = torch.library.Library(_NS, "DEF")
 
-# --- reference schemas (pybind.cpp:52-75), unchanged ---
+# --- reference schemas (pybind.cpp:52-75); one annotation added: the kernel writes k_pre_rope
+# (fused_qknorm_rope_3d_kernel.cu:97-100), which the reference schema leaves undeclared, so under
+# torch.compile functionalisation would not see that write. Declaring it mutable keeps every call
+# site valid and makes the write visible. ---
 _lib_def.define(
     "fused_qk_norm_rope_3d_paired(Tensor! q, Tensor! k, int seq_len, int num_heads, float eps, "
-    "Tensor q_weight, Tensor k_weight, Tensor cos, Tensor sin, Tensor? k_pre_rope) -> ()")
+    "Tensor q_weight, Tensor k_weight, Tensor cos, Tensor sin, Tensor(a!)? k_pre_rope) -> ()")
 _lib_def.define(
     "fused_joint_qkv_pack(Tensor img_q, Tensor img_k, Tensor img_v, "
     "Tensor txt_q, Tensor txt_k, Tensor txt_v, Tensor? cached_k, Tensor? cached_v, "

@@ -49,6 +49,7 @@ _view = ctypes.POINTER(Bf16View)
 SIGNATURES = {
     "joy_abi_version": (_int, []),
     "joy_last_error": (ctypes.c_char_p, []),
+    "joy_init": (_int, []),
     "joy_per_token_quant_fp8": (_int, [_vp, _int, _vp, _vp, _i64, _i64, _int, _vp]),
     "joy_fp8_scaled_mm": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _int, _i64, _i64, _i64, _int, _vp, _i64, _vp]),
     "joy_fp8_scaled_mm_workspace_size": (_i64, [_i64, _i64, _i64]),
@@ -75,7 +76,7 @@ SIGNATURES = {
                _vp]),
 }
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 
 class JoyError(RuntimeError):

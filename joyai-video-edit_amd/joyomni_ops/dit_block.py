@@ -25,7 +25,8 @@ per stream (video "img", condition "txt"), with ``mod = table + vec`` split into
     (``fused_text_qkv_pack``);
 * attention: the gfx950 flash-attention kernel (``sdpa_attention``), non-causal, no
   mask, default scale 1/sqrt(D) -- the reference's ``_sdpa_attention``
-  (``dit.py:154-167``) read in the token-major joint layout without transposes;
+  (``dit.py:154-167``) read in the token-major joint layout without transposes
+  (``attention_backend="torch_sdpa"`` runs the reference's own call instead);
 * out-proj FP8 GEMM with the gated residual (``fused_add_gate``, ``dit.py:525-528``)
   in its epilogue (``fp8_scaled_mm_gated_residual``);
 * adaLN + FP8 quant -> FFN-up FP8 GEMM with the GELU-tanh epilogue -> quant ->
@@ -140,7 +141,9 @@ class JointKV:
     same assembly across the denoising steps of a chunk (``dit.py:1168-1217``,
     ``_assemble_layer_kv_cache_cached`` ``dit.py:801-816``) and copies it into the joint
     buffers on every call (``fused_joint_qkv_pack``, ``dit.py:489-496``); here the rows stay
-    where the attention reads them and only the video and condition rows are rewritten."""
+    where the attention reads them and only the video and condition rows are rewritten. The
+    stamp holds the ring and every RoPE table it names (compared by identity), so these stay
+    alive while the JointKV does and a table rebuilt at a recycled address never matches."""
     k: Optional[torch.Tensor] = None
     v: Optional[torch.Tensor] = None
     stamp: Optional[tuple] = None
@@ -149,17 +152,42 @@ class JointKV:
         self.stamp = None
 
 
+class _Same:
+    """A stamp entry that holds a strong reference to an object and compares by identity.
+
+    Holding the reference keeps the object (a ring, a RoPE table) alive for as long as the stamp
+    is, so its address cannot be handed to a new tensor with other contents while a stamp that
+    names it exists; comparing by ``is`` then tells a rebuilt table from the original even where
+    address, shape, strides and version counter all agree."""
+
+    __slots__ = ("obj",)
+
+    def __init__(self, obj):
+        self.obj = obj
+
+    def __eq__(self, other):
+        return isinstance(other, _Same) and other.obj is self.obj
+
+    def __hash__(self):
+        return id(self.obj)
+
+    def __repr__(self):
+        return f"_Same({type(self.obj).__name__}@{id(self.obj):#x})"
+
+
 def _tensor_key(t: Optional[torch.Tensor]):
     if t is None:
         return None
-    return (t.data_ptr(), tuple(t.shape), tuple(t.stride()), str(t.dtype), t._version)
+    return (_Same(t), t.data_ptr(), tuple(t.shape), tuple(t.stride()), str(t.dtype), t._version)
 
 
 def cached_rows_stamp(ring: Optional[KVRing], cached: Sequence[CachedChunk]) -> tuple:
-    """Everything the assembled cached rows depend on; equal stamps mean equal rows."""
+    """Everything the assembled cached rows depend on; equal stamps mean equal rows. The stamp
+    holds the ring, its K / V tensors and every table it names (compared by identity), so a
+    table freed and rebuilt with other values at the same address never matches."""
     if not cached:
         return ()
-    return (id(ring), ring.k.data_ptr(), ring.k._version, ring.v._version,
+    return (_Same(ring), _Same(ring.k), _Same(ring.v), ring.k.data_ptr(), ring.k._version, ring.v._version,
             tuple((c.slot, ring.lengths[c.slot], ring.pre_rope[c.slot], ring.generation[c.slot],
                    _tensor_key(c.cos), _tensor_key(c.sin)) for c in cached))
 
@@ -180,7 +208,13 @@ class QuantizedDoubleStreamBlock:
     """The quantised chain of one two-stream MMDiT block (see the module docstring)."""
 
     def __init__(self, hidden: int, heads: int, mlp_hidden: int, device, generator: torch.Generator,
-                 quant_rounding: str = "reference_rocm", overlap_streams: bool = True):
+                 quant_rounding: str = "reference_rocm", overlap_streams: bool = True,
+                 attention_backend: str = "hip"):
+        if attention_backend not in ("hip", "torch_sdpa"):
+            raise ValueError(f"attention_backend must be 'hip' or 'torch_sdpa', not {attention_backend!r}")
+        # "hip": this library's attention kernel on the token-major joint operands; "torch_sdpa": the
+        # reference's own call, F.scaled_dot_product_attention on transposed views (dit.py:154-167)
+        self.attention_backend = attention_backend
         self.hidden, self.heads, self.mlp_hidden = hidden, heads, mlp_hidden
         self.head_dim = hidden // heads
         self.quant_rounding = quant_rounding
@@ -211,9 +245,12 @@ class QuantizedDoubleStreamBlock:
                                    exact_division_for(k_in, self.quant_rounding))
         return q, s
 
-    @staticmethod
-    def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
-        """Attention on [B, S, H, D] operands (dit.py:154-167): [B, S, H, D] out, heads dense."""
+    def attention(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+        """Attention on [B, S, H, D] operands (dit.py:154-167): [B, S, H, D] out."""
+        if self.attention_backend == "torch_sdpa":
+            out = torch.nn.functional.scaled_dot_product_attention(
+                q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), is_causal=False)
+            return out.transpose(1, 2)
         return sdpa_attention(q, k, v)
 
     # -- argument checks ----------------------------------------------------

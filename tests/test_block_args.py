@@ -121,3 +121,36 @@ def test_cached_rows_stamp_tracks_every_input_of_the_assembly():
     for st in changes:
         assert st not in seen, st
         seen.append(st)
+
+
+def test_cached_rows_stamp_holds_its_tables_and_tells_a_rebuilt_table_at_the_same_address():
+    """A table built per forward and dropped on return may have its address handed to the next
+    forward's table. The stamp keeps every table it names alive (so the address cannot be
+    recycled while the stamp exists) and compares them by identity: a different tensor with the
+    same address, shape, strides, dtype and version counter but other contents does not match."""
+    import gc
+    import weakref
+
+    from joyomni_ops.dit_block import cached_rows_stamp
+    r = _ring()
+    cos, sin = _tables(16)
+    ref = weakref.ref(cos)
+    # a tensor aliasing the same memory with the same data_ptr, shape, strides, dtype and version
+    # counter (set_ leaves the alias at version 1; one in-place no-op puts the table there too)
+    alias = torch.empty(0).set_(cos.untyped_storage(), cos.storage_offset(), cos.shape, cos.stride())
+    cos.mul_(1.0)
+    assert alias.data_ptr() == cos.data_ptr() and alias._version == cos._version == 1
+    stamp = cached_rows_stamp(r, [CachedChunk(0, cos, sin)])
+    alias.numpy()[:] = 0.25                      # a raw write that no version counter sees
+    assert cached_rows_stamp(r, [CachedChunk(0, alias, sin)]) != stamp
+    assert cached_rows_stamp(r, [CachedChunk(0, cos, sin)]) == stamp
+    del cos, alias
+    gc.collect()
+    assert ref() is not None                     # the stamp keeps the table (and its address) alive
+    del stamp
+    gc.collect()
+    assert ref() is None
+    # a ring rebuilt from scratch (generations reset to 0) is another ring
+    r2 = _ring()
+    c2, s2 = _tables(16)
+    assert cached_rows_stamp(r2, [CachedChunk(0, c2, s2)]) != cached_rows_stamp(r, [CachedChunk(0, c2, s2)])

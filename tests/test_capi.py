@@ -231,3 +231,9 @@ def test_attention_argument_checks(lib):
     _status(lib, f(b(V(0x1008, 8, 256, 128)), b(keys), b(keys), out, 256, 2, 128, 0.1, None), 2,
             "16-byte aligned rows")
     assert f(b(V(0, 0, 256, 128)), b(keys), b(keys), out, 256, 2, 128, 0.1, None) == 0  # no queries: no launch
+
+
+def test_init_is_ok_without_a_device(lib):
+    """joy_init resolves per-device state for every visible device; with none visible (this CPU
+    container) it has nothing to do and returns JOY_OK."""
+    assert lib.joy_init() == _lib.JOY_OK, lib.joy_last_error()

@@ -202,18 +202,20 @@ def test_block_chain_full_size_cfg4():
 
 def test_block_overlapped_streams_match_serial():
     """The condition stream on its own HIP stream (the default) gives the same bits as the serial
-    chain at the cfg-4 workload: outputs of both streams and the written ring slot, for serial
-    calls and for three overlapped calls queued back to back without a host synchronisation (the
-    second stream's buffers are reused across the queued blocks)."""
+    chain at the cfg-4 workload: outputs of both streams and the written ring slot for three
+    overlapped calls queued back to back without a host synchronisation, each on its own inputs
+    (video, condition and modulation vector differ per call), against serial calls on the same
+    inputs. With different inputs per call, a side stream that read a buffer of the previous call
+    (q/k/v, the attention output, a recycled allocator block) before the main stream rewrote it
+    would show as a difference."""
     from joyomni_ops.dit_block import CachedChunk, KVRing, QuantizedDoubleStreamBlock
     announce("block overlapped streams vs serial")
     E, H, FFN, T, hh, ww = 5120, 40, 13824, 512, 45, 80
     L, D = 3 * hh * ww, E // H
     g = gen(606)
     blk = QuantizedDoubleStreamBlock(E, H, FFN, DEV, g)
-    img = torch.randn(1, L, E, generator=g).to(torch.bfloat16).to(DEV)
-    txt = torch.randn(1, T, E, generator=g).to(torch.bfloat16).to(DEV)
-    vec = torch.randn(1, E, generator=g).to(torch.bfloat16).to(DEV)
+    inputs = [tuple(torch.randn(*shape, generator=g).to(torch.bfloat16).to(DEV)
+                    for shape in ((1, L, E), (1, T, E), (1, E))) for _ in range(3)]
     cos_h, sin_h = (t.to(DEV) for t in _half_tables([6, 7, 8], hh, ww))
     cf, sf = (t.to(DEV) for t in _full_tables(list(range(6)), hh, ww))
     ring = KVRing(4, L, H, D, DEV)
@@ -224,19 +226,22 @@ def test_block_overlapped_streams_match_serial():
         ring.lengths[slot] = L
         cached.append(CachedChunk(slot, cf[c * L:(c + 1) * L], sf[c * L:(c + 1) * L]))
 
-    def run():
+    def run(img, txt, vec):
         oi, ot = blk.forward(img, txt, vec, cos_h, sin_h, ring=ring, write_slot=0, cached=cached)
         return [t.clone().view(torch.int16) for t in (oi, ot, ring.k[0], ring.v[0])]
 
     blk.overlap_streams = False
-    ref = run()
-    torch.cuda.synchronize()
+    refs = []
+    for x in inputs:
+        refs.append(run(*x))
+        torch.cuda.synchronize()
     blk.overlap_streams = True
-    got = [run() for _ in range(3)]
+    got = [run(*x) for x in inputs]
     torch.cuda.synchronize()
-    for i, outs in enumerate(got):
+    for i, (outs, ref) in enumerate(zip(got, refs)):
         for name, a, b in zip(("img", "txt", "ring k", "ring v"), outs, ref):
             assert torch.equal(a, b), f"overlapped call {i}: {name} differs from the serial chain"
+    assert not torch.equal(refs[0][0], refs[1][0]) and not torch.equal(refs[1][1], refs[2][1])
 
 
 def test_block_chain_reference_production_geometry():
@@ -379,3 +384,33 @@ def test_block_image_only_forward(mixed):
     f_v, e_v = ulp_frac(ring.v[0, :n].cpu(), rv)
     assert f_k <= 1e-3 and e_k <= 1e-2 and f_v <= 1e-3 and e_v <= 1e-2, (f_k, e_k, f_v, e_v)
     assert not ring.k[0, n:].any() and ring.lengths[0] == n
+
+
+def test_block_torch_sdpa_backend_matches_hip_attention():
+    """attention_backend="torch_sdpa" (the reference's F.scaled_dot_product_attention call, as the
+    benchmark's cfg-4 block line with SDPA uses it) gives the block of the HIP attention kernel up
+    to the attention's rounding: same weights and inputs, the two block updates within 3e-2 of the
+    update's RMS (the chain re-quantises after attention, see the module docstring)."""
+    from joyomni_ops.dit_block import CachedChunk, KVRing, QuantizedDoubleStreamBlock
+    announce("block torch_sdpa backend vs hip attention")
+    E, H, FFN, T, hh, ww = 512, 4, 1536, 32, 12, 20
+    L, D = hh * ww, E // H
+    img = torch.randn(1, L, E, generator=gen(707)).to(torch.bfloat16).to(DEV)
+    txt = torch.randn(1, T, E, generator=gen(708)).to(torch.bfloat16).to(DEV)
+    vec = torch.randn(1, E, generator=gen(709)).to(torch.bfloat16).to(DEV)
+    cos_h, sin_h = (t.to(DEV) for t in _half_tables([3], hh, ww))
+    cf, sf = (t.to(DEV) for t in _full_tables([0], hh, ww))
+    outs = []
+    for backend in ("hip", "torch_sdpa"):
+        blk = QuantizedDoubleStreamBlock(E, H, FFN, DEV, gen(710), attention_backend=backend)
+        ring = KVRing(2, L, H, D, DEV)
+        ring.k[1].copy_(torch.randn(L, H, D, generator=gen(711)).to(torch.bfloat16))
+        ring.v[1].copy_(torch.randn(L, H, D, generator=gen(712)).to(torch.bfloat16))
+        ring.lengths[1] = L
+        outs.append(blk.forward(img, txt, vec, cos_h, sin_h, ring=ring, write_slot=0,
+                                cached=[CachedChunk(1, cf, sf)]))
+    torch.cuda.synchronize()
+    for (a, b), base in zip(zip(*outs), (img, txt)):
+        assert rms_rel(b, a, base) <= 3e-2
+    with pytest.raises(ValueError, match="attention_backend"):
+        QuantizedDoubleStreamBlock(E, H, FFN, DEV, gen(710), attention_backend="flash4")

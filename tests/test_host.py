@@ -18,8 +18,11 @@ def test_reference_schemas_registered():
     s = str(torch.ops.joyomni_ops.fp8_scaled_mm.default._schema)
     assert "ScalarType out_dtype" in s and "Tensor? bias" in s
     s = str(torch.ops.joyomni_ops.fused_qk_norm_rope_3d_paired.default._schema)
-    assert s.startswith("joyomni_ops::fused_qk_norm_rope_3d_paired(Tensor(") and "Tensor? k_pre_rope" in s
-    assert torch.ops.joyomni_ops.fused_qk_norm_rope_3d_paired.default._schema.arguments[0].alias_info.is_write
+    assert s.startswith("joyomni_ops::fused_qk_norm_rope_3d_paired(Tensor(") and "Tensor(a!)? k_pre_rope" in s
+    args = torch.ops.joyomni_ops.fused_qk_norm_rope_3d_paired.default._schema.arguments
+    # q, k (as in the reference) and k_pre_rope (which the reference's kernel writes but its schema
+    # leaves undeclared) are declared mutable
+    assert [a.name for a in args if a.alias_info is not None and a.alias_info.is_write] == ["q", "k", "k_pre_rope"]
 
 
 def test_fake_kernels_shapes():

@@ -1,8 +1,9 @@
 """GPU: the allocation-free FP8 GEMM entry point (joy_fp8_scaled_mm_noalloc) against the
 workspace entry point (joy_fp8_scaled_mm), through the C ABI. Both run the same kernels and the
-same split-K plan, so the outputs must be bit-identical: calls in a row (the second on a
-smaller problem, so stale partial sums of the first would show), a problem that needs no
-scratch, and the largest split plan of the device, which fills the whole scratch."""
+same split-K plan, so the outputs must be bit-identical: the first call of the process captured
+into a HIP graph and replayed, calls in a row (the second on a smaller problem, so stale partial
+sums of the first would show), a problem that needs no scratch, and the largest split plan of
+the device, which fills the whole scratch on a 256-CU MI355X."""
 import ctypes
 
 import numpy as np
@@ -46,6 +47,44 @@ def _both(lib, M, N, K, epilogue, seed):
     return need, ref, got
 
 
+def test_noalloc_first_call_captured_in_a_graph():
+    """The first joy_fp8_scaled_mm_noalloc call of the process, captured into a HIP graph after
+    joy_init() (which resolves the scratch address, so the captured call makes no runtime query),
+    replayed three times with eager work between the replays (a NaN fill of the output and an
+    eager no-alloc call on another problem, which leaves other partial sums in the scratch):
+    every replay equals the workspace entry point bit for bit. A split-K plan, so the replays
+    read and write the scratch. This test runs before the file's other no-alloc calls."""
+    import joyomni_ops as jo
+    from joyomni_ops import _lib
+    lib = jo._LIB
+    _lib.check(lib, lib.joy_init())
+    M, N, K = 256, 5120, 5120
+    announce("noalloc gemm under graph capture", M, N, K)
+    a, w, sa, sw, bias = _problem(M, N, K, 300)
+    need = lib.joy_fp8_scaled_mm_workspace_size(M, N, K)
+    assert need > 0
+    ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+    ref = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+    _lib.check(lib, _call(lib, "joy_fp8_scaled_mm", a, w, sa, sw, bias, ref, M, N, K, 0, ws.data_ptr(), need))
+    got = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=DEV)
+    other = _problem(64, 5120, 5120, 301)
+    other_out = torch.empty((64, 5120), dtype=torch.bfloat16, device=DEV)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            _lib.check(lib, _call(lib, "joy_fp8_scaled_mm_noalloc", a, w, sa, sw, bias, got, M, N, K, 0))
+    torch.cuda.synchronize()
+    for i in range(3):
+        got.fill_(float("nan"))
+        _lib.check(lib, _call(lib, "joy_fp8_scaled_mm_noalloc", *other, other_out, 64, 5120, 5120, 0))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), f"replay {i}"
+
+
 def test_noalloc_matches_workspace_entry_point():
     import joyomni_ops as jo
     lib = jo._LIB
@@ -75,6 +114,9 @@ def test_noalloc_uses_the_whole_scratch_and_every_plan_fits():
     M, N, K = 512, 4096, 8192
     announce("noalloc gemm full scratch", M, N, K)
     need, ref, got = _both(lib, M, N, K, 0, 200)
-    assert need == worst == cap, (need, worst, cap)
+    assert 0 < need <= worst <= cap, (need, worst, cap)
+    # the bound is "every plan fits"; on a 256-CU MI355X the largest plan fills the scratch exactly
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert need == worst == cap, (need, worst, cap)
     assert not torch.isnan(ref.float()).any()
     assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
