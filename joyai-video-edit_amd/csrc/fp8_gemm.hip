@@ -13,8 +13,9 @@
 // sgl_fused_ops.py:302-305); residual and output may be the same buffer.
 //
 // Kernels by problem shape:
-//  * fp8_gemm_4p (K % 256 == 0, M % 4 == 0, M > 512): persistent 256x256 tiles, one
-//    workgroup per CU walking the whole rounds, 128-byte K steps through a 2-slot ring;
+//  * fp8_gemm_4q (K % 256 == 0, M % 4 == 0, M > 512): persistent 256x256 tiles, one
+//    workgroup per CU walking the whole rounds, 128-byte K steps through a 2-slot ring,
+//    16x16x128 MFMAs;
 //  * fp8_gemm_4k (M <= 512, and long-K GEMMs of less than one round): deep-K tiles
 //    with register-staged operands and optional split-K;
 //  * fp8_gemm_4h (K % 128 == 0): one 256x128 or 128x128 tile per workgroup with the
@@ -342,7 +343,8 @@ __device__ __forceinline__ void sched_pattern() {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
     constexpr int RD = (R + N - 1) / N;
     if constexpr (I * RD < R) __builtin_amdgcn_sched_group_barrier(0x100, RD, 0);  // LDS reads
-    if constexpr (I < L) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);        // one DMA
+    constexpr int LD = (L + N - 1) / N;
+    if constexpr (I * LD < L) __builtin_amdgcn_sched_group_barrier(0x020, LD, 0);  // DMAs
     sched_pattern<I + 1, N, R, L>();
   }
 }
@@ -631,35 +633,11 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 // ---------------------------------------------------------------------------
-// Persistent variant of the 256x256 bulk launch (plain and GELU epilogues): gridDim.x
-// workgroups (a multiple of 8, one per CU) each walk the tiles b, b + gridDim.x, ... of
-// the XCD-ordered grouped tile order. The operand ring runs on across tiles: during the
-// last 2 K steps of a tile the ring fetches the next tile's first 2 steps, so a new tile
-// starts on data already in LDS, and the epilogue's stores drain while the next tile's
-// MFMAs run.
-//
-//   * K steps of 128 bytes in a ring of S = 2 slots of 64 KiB: every operand row of a step
-//     is one 128-byte request (with 64-byte steps and a 4-slot ring the same kernel made
-//     twice the L2 requests and ran 2-6 % slower on the cfg-2 GEMMs: QKV 748 -> 706 us,
-//     out-projection 260 -> 253, FFN-up + GELU 727 -> 681, FFN-down 636 -> 622, bit-identical).
-//     Step t (slot t & 1): the MFMAs of its first 64-byte half while the second half's
-//     fragments are read; wait for step t + 1 and one barrier; the DMA of step t + 2 into
-//     slot t & 1 (whose reads every wave has finished); the MFMAs of the second half while
-//     the first half of step t + 1 is read. A step's DMA thus has one step (32 MFMAs per
-//     wave) to land. Steps go through buffer loads straight into LDS (row offsets are
-//     32-bit: M*K, N*K < 2^31).
-//   * Per-tile column scales, bias and row scales arrive by one DMA per wave with the
-//     tile's step 2 into side_lds; the epilogue stages 16-row chunks of the wave's
-//     128x128 sub-tile through its own 4 KiB of stage_lds and stores 16-byte row segments
-//     with buffer stores (out-of-range lanes get an offset past the buffer, so every
-//     wave issues exactly NST stores per tile, whatever M and N).
-//   * vmcnt is in order on gfx9 for loads and stores alike, so each wait is a constant:
-//     none of a step's own DMAs may be outstanding when the next step is read, except in
-//     a tile's first step, whose wait (for step 1, fetched during the previous tile) also
-//     counts the NST epilogue stores issued after it.
-//   * The DMAs are inline asm: the compiler does not track them (through the builtins
-//     it cannot tell an epilogue LDS access from the ring slots the DMAs write and
-//     waits for every DMA in flight). m0 is written only by those asm statements.
+// Direct-to-LDS operand loads of the persistent and one-tile 128-byte-step kernels. They are
+// inline asm: the compiler does not track them (through the builtins it cannot tell an
+// epilogue LDS access from the ring slots the DMAs write and waits for every DMA in flight).
+// m0 is written only by these asm statements. vmcnt is in order on gfx9 for loads and stores
+// alike, so the kernels wait on constant counts.
 // ---------------------------------------------------------------------------
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
@@ -683,32 +661,86 @@ __device__ __forceinline__ void wait_vmcnt_lgkm0() {
   __builtin_amdgcn_s_waitcnt((W & 15) | ((W >> 4) << 14) | 0x0070);
 }
 
-template <bool kBf16, int kEpi>
-__global__ __launch_bounds__(256, 1) void fp8_gemm_4p(
+// ---------------------------------------------------------------------------
+// Persistent bulk kernel (plain, GELU and gated-residual epilogues): gridDim.x workgroups
+// (a multiple of 8, one per CU) each walk the tiles b, b + gridDim.x, ... of the XCD-ordered
+// grouped tile order. The operand ring runs on across tiles: during the last 2 K steps of a
+// tile the ring fetches the next tile's first 2 steps, so a new tile starts on data already in
+// LDS, and the epilogue's stores drain while the next tile's MFMAs run.
+//
+//   * K steps of 128 bytes in a ring of S = 2 slots: every operand row of a step is one
+//     128-byte request (a 64-byte-step ring of the same kernel made twice the L2 requests and
+//     ran 2-6 % slower on the cfg-2 GEMMs). Steps go through buffer loads straight into LDS
+//     (row offsets are 32-bit: M*K, N*K < 2^31); a step's DMA is issued during step t - 2's
+//     second phase and waited for in step t - 1, so it has one step to land.
+//   * Per-tile column scales, bias and row scales arrive by one DMA per wave with the tile's
+//     step 2 into side_lds.
+//   * Each wait is a constant count: none of a step's own DMAs may be outstanding when the
+//     next step is read, except in a tile's first step, whose wait (for step 1, fetched during
+//     the previous tile) also counts the NST epilogue stores issued after it.
+//   * MFMA: v_mfma_scale_f32_16x16x128_f8f6f4, 16 x 16 tiles that each consume a whole
+//     128-byte K step. On random e4m3 operands this instruction sustains a higher shader clock
+//     than 32x32x64 at the same MFMA density (MI355X, one wave per SIMD, operands in registers:
+//     2.04 vs 1.87 GHz, both 100 % MFMA-busy; re-read from LDS every step: 1.98 vs 1.83 GHz),
+//     i.e. it draws less power per FLOP, and the part runs these GEMMs power-limited. The
+//     accumulated sums are the 32x32x64 kernels' to the bit on every GEMM test.
+//
+// Tile BM x BN (BM = 256, BN = 128, 192 or 256), 4 waves in 2 x 2, each a 128 x (BN/2)
+// sub-tile = 8 x FN MFMA tiles of 16 x 16 (FN = BN/32; 4 fp32 accumulators each). Operand
+// lanes: lane l holds row l % 16 of its fragment, K bytes [32 (l / 16), +32) of the step;
+// accumulator lane l, element e = output (m = l % 16, n = 4 (l / 16) + e) of its tile (the
+// MFMA's "A" operand is W, its "B" operand the activations).
+//
+// Step t (slot t & 1), two phases of FH x 8 MFMAs (FH = FN / 2):
+//   A: W fragments [0, FH) x every A fragment, i-major, while W fragments [FH, FN) of step t
+//      are read from the slot;
+//   wait for step t + 1, one barrier;
+//   B: W fragments [FH, FN) x every A fragment, j-major; after column j's MFMAs its A registers
+//      take fragment j of step t + 1, W fragments [0, FH) of step t + 1 are read alongside (both
+//      from the other slot), and an eighth of the DMAs of step t + 2 into this slot are issued.
+// Registers: 8 x FN x 4 accumulators (AGPRs) + FN + 8 fragments of 8 VGPRs (128 at BN = 256).
+// The epilogue stages each 16-row chunk of the wave's sub-tile through a padded LDS area
+// (row pitch BN + 16 bytes: the 8-byte writes of 16 rows and the 16-byte row reads each
+// cover distinct banks) and stores 16-byte row segments with buffer stores, NSTC per chunk
+// for every wave whatever M and N (out-of-range lanes store past the buffer's range).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ v4f mfma_16x16x128_fp8(const v8i& a, const v8i& b, const v4f& c) {
+  // Scale operands of zero select the plain (unscaled) f8f6f4 MFMA; format 0 = e4m3.
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+template <bool kBf16, int kEpi, int BN>
+__global__ __launch_bounds__(256, 1) void fp8_gemm_4q(
     const uint8_t* __restrict__ A, const uint8_t* __restrict__ W, const float* __restrict__ sa,
     const float* __restrict__ sb, const uint16_t* __restrict__ bias, uint16_t* __restrict__ C,
     int M, int N, int K, int64_t ldc, int tiles_m, int tiles_n, int group_m, int ntiles, ResidualArgs res) {
   static_assert(kEpi == kEpiPlain || kEpi == kEpiGelu || kEpi == kEpiResidual, "plain, GELU, gated residual");
-  constexpr int BM = 256, BN = 256, KS = 128, NW = 4, S = 2;
-  constexpr int WTM = BM / 2, WTN = BN / 2, FM = WTM / 32, FN = WTN / 32;
+  static_assert(BN == 128 || BN == 192 || BN == 256, "tile widths");
+  constexpr int BM = 256, KS = 128, NW = 4, S = 2;
+  constexpr int WTM = BM / 2, WTN = BN / 2, FM = WTM / 16, FN = WTN / 16, FH = FN / 2;
   constexpr int CPR = KS / 16, RPL = 64 / CPR;  // 8 chunks per row, 8 rows per DMA instruction
   constexpr int IA = BM / RPL / NW, IW = BN / RPL / NW, LOADS = IA + IW;
   constexpr int A_BYTES = BM * KS, SLOT = (BM + BN) * KS;
-  constexpr int NMFMA = FM * FN, NREAD = 2 * (FM + FN);
-  constexpr int NST = WTM * WTN * 2 / 1024;
-  constexpr int CROWS = 16;
-  constexpr int STAGE = CROWS * WTN * 2;
+  constexpr int CPL = WTN / 8;             // 16-byte chunks of a staged row
+  constexpr int PITCH = WTN * 2 + 16;      // staged row pitch
+  constexpr int NSTC = 16 * CPL / 64;      // stores per 16-row chunk and wave
+  constexpr int NST = FM * NSTC;           // stores per tile and wave
+  constexpr int STAGE = 16 * PITCH;
+  static_assert(FN % 2 == 0 && (16 * CPL) % 64 == 0, "phases and store shapes");
   static_assert(S * SLOT + 4096 + NW * STAGE <= 160 * 1024, "LDS");
   static_assert(LOADS + NST + 1 < 64, "vmcnt range");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[S * SLOT];
   __shared__ __attribute__((aligned(1024))) uint8_t side_lds[4096];
-  __shared__ __attribute__((aligned(1024))) uint8_t stage_lds[NW * STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t stage_lds[NW * STAGE];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  const int frow = lane & 31, g = lane >> 5;
+  const int frow = lane & 15, g = lane >> 4;
   const int fsw = swz_rows<KS>(frow);
+  // fragment byte offsets of the lane's two 16-byte chunks (logical chunks 2g, 2g + 1; the
+  // swizzle is invariant under row -> row + 16)
+  const int fo0 = ((2 * g) ^ fsw) * 16, fo1 = ((2 * g + 1) ^ fsw) * 16;
   const int a_row0 = (wm * WTM + frow) * KS, w_row0 = A_BYTES + (wn * WTN + frow) * KS;
   const int nk = K / KS;  // even (K % 256 == 0)
   const int P = gridDim.x;
@@ -717,7 +749,6 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4p(
       __builtin_amdgcn_make_buffer_rsrc(C, 0, (int)(((int64_t)(M - 1) * ldc + N) * 2), 0x00020000);
   const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, (int)((int64_t)M * K), 0x00020000);
   const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc((void*)W, 0, (int)((int64_t)N * K), 0x00020000);
-  // gated residual (residual rows may be C itself) and gate; out-of-range offsets read zeros
   const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)res.ptr, 0, kEpi == kEpiResidual ? (int)(((int64_t)(M - 1) * res.ld + N) * 2) : 0, 0x00020000);
   const __amdgpu_buffer_rsrc_t grs =
@@ -734,8 +765,7 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4p(
 #pragma unroll
     for (int i = 0; i < IA; ++i) {
       const int row = (wave * IA + i) * RPL + lrow;
-      // rows past M fall outside the descriptor's range and load zeros (not stored; zero operands
-      // also draw less power than copies of the last row)
+      // rows past M (N) fall outside the descriptor's range and load zeros (never stored)
       oa[i] = (uint32_t)(mm + row) * (uint32_t)K + (uint32_t)((lchunk ^ swz_rows<KS>(row)) * 16);
     }
 #pragma unroll
@@ -761,77 +791,80 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4p(
     dma_glb16(lds_u32((lds_void*)(side_lds + wave * 1024)), src);
   };
 
-  v16f acc[FN][FM];
-  v8i fwx[FN], fax[FM], fwy[FN], fay[FM];
-  // fragments of 64-byte half h of the step in `slot`
-  auto read_frags = [&](int slot, int h, v8i (&fw)[FN], v8i (&fa)[FM]) {
-    const uint8_t* base = lds + slot * SLOT;
-    const int o0 = ((4 * h + 2 * g) ^ fsw) * 16, o1 = ((4 * h + 2 * g + 1) ^ fsw) * 16;
-#pragma unroll
-    for (int f = 0; f < FN; ++f) {
-      const uint8_t* r = base + w_row0 + f * 32 * KS;
-      const v4i lo = *(const v4i*)(r + o0);
-      const v4i hi = *(const v4i*)(r + o1);
-      fw[f] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-    }
-#pragma unroll
-    for (int f = 0; f < FM; ++f) {
-      const uint8_t* r = base + a_row0 + f * 32 * KS;
-      const v4i lo = *(const v4i*)(r + o0);
-      const v4i hi = *(const v4i*)(r + o1);
-      fa[f] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-    }
+  v4f acc[FN][FM];
+  v8i fw[FN], fa[FM];
+  auto frag = [&](const uint8_t* r) {
+    const v4i lo = *(const v4i*)(r + fo0);
+    const v4i hi = *(const v4i*)(r + fo1);
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   };
-  auto mfmas = [&](const v8i (&fw)[FN], const v8i (&fa)[FM], auto zero) {
-#pragma unroll
-    for (int i = 0; i < FN; ++i)
-#pragma unroll
-      for (int j = 0; j < FM; ++j) {
-        if constexpr (decltype(zero)::value)
-          acc[i][j] = mfma_32x32x64_fp8(fw[i], fa[j], (v16f){});
-        else
-          acc[i][j] = mfma_32x32x64_fp8(fw[i], fa[j], acc[i][j]);
-      }
+  auto mma = [&](int i, int j, auto zero) {
+    if constexpr (decltype(zero)::value)
+      acc[i][j] = mfma_16x16x128_fp8(fw[i], fa[j], (v4f){});
+    else
+      acc[i][j] = mfma_16x16x128_fp8(fw[i], fa[j], acc[i][j]);
   };
   using F = std::false_type;
   using T_ = std::true_type;
-  // one 128-byte step in slot SL: half 0 (fragments X) with the reads of half 1 (into Y); wait for
-  // the next step (outstanding vmcnt `wait`), barrier; DMA `koff` into this slot (and the side
-  // operands); half 1 (Y) with the reads of the next step's half 0 (into X) unless it is the
-  // tile's last step (the next tile's first fragments are read after the epilogue, so that no
-  // fragment registers are live across it)
   auto step = [&](auto slotc, auto zero, auto wait, bool side, int koff, auto nextc) {
     constexpr int SL = decltype(slotc)::value;
+    constexpr bool NEXT = decltype(nextc)::value;
+    const uint8_t* wcur = lds + SL * SLOT + w_row0;
+    const uint8_t* anext = lds + (SL ^ 1) * SLOT + a_row0;
+    const uint8_t* wnext = lds + (SL ^ 1) * SLOT + w_row0;
+    // phase A: W fragments [0, FH) x every A fragment, reading this step's W fragments [FH, FN)
     __builtin_amdgcn_sched_barrier(0);
-    read_frags(SL, 1, fwy, fay);
-    mfmas(fwx, fax, zero);
-    sched_pattern<0, NMFMA, NREAD, 0>();
+#pragma unroll
+    for (int f = FH; f < FN; ++f) fw[f] = frag(wcur + f * 16 * KS);
+#pragma unroll
+    for (int i = 0; i < FH; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j) mma(i, j, zero);
+    sched_pattern<0, FH * FM, (FN - FH) * 2, 0>();
     __builtin_amdgcn_sched_barrier(0);
     wait_vmcnt_lgkm0<decltype(wait)::value>();
     block_barrier();
     __builtin_amdgcn_sched_barrier(0);
     if (side) issue_side(m0, n0);
-    issue(SL, koff);
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (decltype(nextc)::value) {
-      read_frags(SL ^ 1, 0, fwx, fax);
-      mfmas(fwy, fay, F{});
-      sched_pattern<0, NMFMA, NREAD, 0>();
-    } else {
-      mfmas(fwy, fay, F{});
+    // phase B: W fragments [FH, FN) x A fragment j, j-major; once column j is issued, its A
+    // registers take the next step's fragment j, and the next step's W fragments [0, FH) (free
+    // since phase A) are read alongside. The DMAs of step t + 2 into this slot are spread over
+    // the columns, LOADS / FM after each: issued as one block after the barrier they left the
+    // MFMAs idle while the four waves queued 4 x LOADS DMA instructions (11 % slower over the
+    // QKV, out-projection and FFN-down GEMMs, bit-identical).
+    const uint32_t dbase = lds_u32((lds_void*)(lds + SL * SLOT));
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+#pragma unroll
+      for (int i = FH; i < FN; ++i) mma(i, j, zero);
+      if constexpr (NEXT) {
+        fa[j] = frag(anext + j * 16 * KS);
+        if (j < FH) fw[j] = frag(wnext + j * 16 * KS);
+      }
+#pragma unroll
+      for (int d = j * LOADS / FM; d < (j + 1) * LOADS / FM; ++d) {
+        if (d < IA)
+          dma_buf16(dbase + (wave * IA + d) * 1024, oa[d], ars, koff);
+        else
+          dma_buf16(dbase + A_BYTES + (wave * IW + d - IA) * 1024, ow[d - IA], wrs, koff);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_sched_barrier(0);
   };
 
-  // prologue: steps 0 and 1 of the first tile, fragments of step 0's first half
+  // prologue: steps 0 and 1 of the first tile
   issue(0, 0);
   issue(1, KS);
   wait_vmcnt<LOADS>();
   block_barrier();
   bool first = true;
   for (;;) {
-    // the first half of step 0 (in slot 0: landed before the last barrier)
-    read_frags(0, 0, fwx, fax);
+    // the first step's A fragments and W fragments [0, FH) (slot 0: landed before the last barrier)
+#pragma unroll
+    for (int f = 0; f < FM; ++f) fa[f] = frag(lds + a_row0 + f * 16 * KS);
+#pragma unroll
+    for (int f = 0; f < FH; ++f) fw[f] = frag(lds + w_row0 + f * 16 * KS);
     // step 0: its wait is for step 1, issued before the previous tile's NST epilogue stores
     if (first) {
       step(IC<0>{}, T_{}, IC<0>{}, true, 2 * KS, T_{});
@@ -863,94 +896,79 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4p(
 
     // epilogue of tile (tm0, tn0)
     {
-      // an opaque copy of the lane index keeps the epilogue's addresses out of the main loop
-      int lane_e;
+      int lane_e;  // an opaque copy of the lane index keeps the epilogue's addresses out of the main loop
       asm volatile("v_mov_b32 %0, %1" : "=v"(lane_e) : "v"(lane));
-      const int er = lane_e & 31, eg = lane_e >> 5;
+      const int er = lane_e & 15, eg = lane_e >> 4;
       const float* sa_l = (const float*)(side_lds);
       const float* sb_l = (const float*)(side_lds + 1024);
       const uint16_t* bias_l = (const uint16_t*)(side_lds + 2048);
       uint8_t* stage = stage_lds + wave * STAGE;
       const int mw = tm0 + wm * WTM, nw0 = tn0 + wn * WTN;
       typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-      // the lane's 8 output columns in the read-back below are fixed for the tile
-      const int n_lane = nw0 + (lane_e & 15) * 8;
-      u32x4 gv = {0, 0, 0, 0};
-      if constexpr (kEpi == kEpiResidual)
-        gv = __builtin_amdgcn_raw_buffer_load_b128(grs, n_lane < N ? n_lane * 2 : 0x40000000, 0, 0);
+      // the gate of the 8 output columns each lane stores in read-back instruction k (fixed per tile)
+      u32x4 gv[NSTC];
+#pragma unroll
+      for (int k = 0; k < NSTC; ++k) {
+        gv[k] = (u32x4){0, 0, 0, 0};
+        if constexpr (kEpi == kEpiResidual) {
+          const int n = nw0 + ((k * 64 + lane_e) % CPL) * 8;
+          gv[k] = __builtin_amdgcn_raw_buffer_load_b128(grs, n < N ? n * 2 : 0x40000000, 0, 0);
+        }
+      }
 #pragma unroll
       for (int j = 0; j < FM; ++j) {
-        // the lane's row er of MFMA tile j, all FN x 4 x 4 columns: scaled, biased, rounded
-        // (and GELU on the rounded value, as the reference applies F.gelu to the GEMM output)
         int jz;  // re-read the column operands per chunk rather than holding them in registers
         asm volatile("v_mov_b32 %0, 0" : "=v"(jz));
-        // gated residual: the 8 residual row segments this lane stores for tile j, loaded before
-        // the chunk's arithmetic so that their latency overlaps it
-        u32x4 rx[2][CROWS / 4];
+        // gated residual: the row segments this lane stores for chunk j, loaded before the chunk's
+        // arithmetic so that their latency overlaps it
+        u32x4 rx[NSTC];
         if constexpr (kEpi == kEpiResidual) {
 #pragma unroll
-          for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int k = 0; k < CROWS / 4; ++k) {
-              const int m = mw + j * 32 + h * 16 + k * 4 + (lane_e >> 4);
-              const uint32_t roff = (m < M && n_lane < N) ? (uint32_t)(((int64_t)m * res.ld + n_lane) * 2) : 0x80000000u;
-              rx[h][k] = __builtin_amdgcn_raw_buffer_load_b128(rrs, (int)roff, 0, 0);
-            }
+          for (int k = 0; k < NSTC; ++k) {
+            const int idx = k * 64 + lane_e, r = idx / CPL, c = idx % CPL;
+            const int m = mw + j * 16 + r, n = nw0 + c * 8;
+            const uint32_t roff = (m < M && n < N) ? (uint32_t)(((int64_t)m * res.ld + n) * 2) : 0x80000000u;
+            rx[k] = __builtin_amdgcn_raw_buffer_load_b128(rrs, (int)roff, 0, 0);
+          }
         }
-        const float s_a = sa_l[wm * WTM + j * 32 + er];
-        uint2 pk[FN][4];
+        const float s_a = sa_l[wm * WTM + j * 16 + er];
+        uint8_t* srow = stage + er * PITCH + eg * 8;
 #pragma unroll
-        for (int i = 0; i < FN; ++i)
+        for (int i = 0; i < FN; ++i) {
+          const int c = wn * WTN + i * 16 + eg * 4;
+          const float4 sv = *(const float4*)(sb_l + c + jz);
+          const uint2 bb = *(const uint2*)(bias_l + c + jz);
+          const float sbe[4] = {sv.x, sv.y, sv.z, sv.w};
+          const float be[4] = {has_bias ? unpack_lo<kBf16>(bb.x) : 0.0f, has_bias ? unpack_hi<kBf16>(bb.x) : 0.0f,
+                               has_bias ? unpack_lo<kBf16>(bb.y) : 0.0f, has_bias ? unpack_hi<kBf16>(bb.y) : 0.0f};
+          float o[4];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int c = wn * WTN + i * 32 + q * 8 + eg * 4;
-            const float4 sv = *(const float4*)(sb_l + c + jz);
-            const uint2 bb = *(const uint2*)(bias_l + c + jz);
-            const float sbe[4] = {sv.x, sv.y, sv.z, sv.w};
-            const float be[4] = {has_bias ? unpack_lo<kBf16>(bb.x) : 0.0f, has_bias ? unpack_hi<kBf16>(bb.x) : 0.0f,
-                                 has_bias ? unpack_lo<kBf16>(bb.y) : 0.0f, has_bias ? unpack_hi<kBf16>(bb.y) : 0.0f};
-            float o[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = __builtin_fmaf(acc[i][j][q * 4 + e] * sbe[e], s_a, be[e]);
-            pk[i][q] = make_uint2(pack2<kBf16>(o[0], o[1]), pack2<kBf16>(o[2], o[3]));
-            if constexpr (kEpi == kEpiGelu) {
-              pk[i][q] = make_uint2(
-                  pack2<kBf16>(gelu_tanh(unpack_lo<kBf16>(pk[i][q].x)), gelu_tanh(unpack_hi<kBf16>(pk[i][q].x))),
-                  pack2<kBf16>(gelu_tanh(unpack_lo<kBf16>(pk[i][q].y)), gelu_tanh(unpack_hi<kBf16>(pk[i][q].y))));
-            }
+          for (int e = 0; e < 4; ++e) o[e] = __builtin_fmaf(acc[i][j][e] * sbe[e], s_a, be[e]);
+          uint2 pk = make_uint2(pack2<kBf16>(o[0], o[1]), pack2<kBf16>(o[2], o[3]));
+          if constexpr (kEpi == kEpiGelu) {
+            pk = make_uint2(pack2<kBf16>(gelu_tanh(unpack_lo<kBf16>(pk.x)), gelu_tanh(unpack_hi<kBf16>(pk.x))),
+                            pack2<kBf16>(gelu_tanh(unpack_lo<kBf16>(pk.y)), gelu_tanh(unpack_hi<kBf16>(pk.y))));
           }
-        // rows h*16 .. h*16+15 of tile j: written by the lanes holding them, read back 4 rows
-        // x 256 bytes per instruction by all lanes, stored as 16-byte row segments
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          if ((er >> 4) == h) {
-            const int rr = er & 15;
-#pragma unroll
-            for (int i = 0; i < FN; ++i)
-#pragma unroll
-              for (int q = 0; q < 4; ++q)
-                *(uint2*)(stage + rr * (WTN * 2) + (((i * 4 + q) ^ rr) * 16) + eg * 8) = pk[i][q];
-          }
-          // other lanes' rows are read next: the compiler must not reuse an earlier read of the
-          // same address (LDS is in order within the wave, so no hardware wait is needed)
-          asm volatile("" ::: "memory");
-#pragma unroll
-          for (int k = 0; k < CROWS / 4; ++k) {
-            const int r = k * 4 + (lane_e >> 4), c = lane_e & 15;
-            uint4 v = *(const uint4*)(stage + r * (WTN * 2) + ((c ^ r) * 16));
-            const int m = mw + j * 32 + h * 16 + r, n = nw0 + c * 8;
-            const uint32_t off = (m < M && n < N) ? (uint32_t)(((int64_t)m * ldc + n) * 2) : 0x80000000u;
-            if constexpr (kEpi == kEpiResidual) {
-              const u32x4 x = rx[h][k];
-              v = make_uint4(gated_pair<kBf16>(v.x, x[0], gv[0]), gated_pair<kBf16>(v.y, x[1], gv[1]),
-                             gated_pair<kBf16>(v.z, x[2], gv[2]), gated_pair<kBf16>(v.w, x[3], gv[3]));
-            }
-            // cache policy 2 = nt: the output is written once (non-temporal stores measured 2.5 %
-            // faster over the cfg-2 GEMMs than default-policy stores)
-            __builtin_amdgcn_raw_buffer_store_b128((u32x4){v.x, v.y, v.z, v.w}, crs, (int)off, 0, 2);
-          }
-          asm volatile("" ::: "memory");
+          *(uint2*)(srow + i * 32) = pk;
         }
+        // other lanes' rows are read next: the compiler must not reuse an earlier read of the same
+        // address (LDS is in order within the wave, so no hardware wait is needed)
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int k = 0; k < NSTC; ++k) {
+          const int idx = k * 64 + lane_e, r = idx / CPL, c = idx % CPL;
+          uint4 v = *(const uint4*)(stage + r * PITCH + c * 16);
+          const int m = mw + j * 16 + r, n = nw0 + c * 8;
+          const uint32_t off = (m < M && n < N) ? (uint32_t)(((int64_t)m * ldc + n) * 2) : 0x80000000u;
+          if constexpr (kEpi == kEpiResidual) {
+            const u32x4 x = rx[k];
+            v = make_uint4(gated_pair<kBf16>(v.x, x[0], gv[k][0]), gated_pair<kBf16>(v.y, x[1], gv[k][1]),
+                           gated_pair<kBf16>(v.z, x[2], gv[k][2]), gated_pair<kBf16>(v.w, x[3], gv[k][3]));
+          }
+          // cache policy 2 = nt: the output is written once
+          __builtin_amdgcn_raw_buffer_store_b128((u32x4){v.x, v.y, v.z, v.w}, crs, (int)off, 0, 2);
+        }
+        asm volatile("" ::: "memory");
       }
     }
     if (!more) break;
@@ -962,10 +980,10 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4p(
 
 // ---------------------------------------------------------------------------
 // One tile per workgroup with 128-byte K steps through an S-slot ring (the sub-tiles of a
-// persistent launch's last round, and single-round direct launches): the step schedule of
-// the persistent kernel -- MFMAs of a step's first 64-byte half while its second half is
-// read, a wait for the next step and one barrier, the DMA of step t + S into the slot just
-// finished, the second half's MFMAs while the next step's first half is read.
+// persistent launch's last round, and single-round direct launches), 32x32x64 MFMAs: the
+// MFMAs of a step's first 64-byte half while its second half is read, a wait for the next
+// step and one barrier, then the second half's MFMAs with the reads of the next step's first
+// half and the DMA of step t + S into the slot just finished spread among them.
 // ---------------------------------------------------------------------------
 template <bool kBf16, int kEpi, int BM, int BN, int S>
 __global__ __launch_bounds__(256, 1) void fp8_gemm_4h(
@@ -1062,12 +1080,39 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4h(
     wait_vmcnt_lgkm0<(S - 2) * LOADS>();
     block_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    issue(slot, kt + S);
-    __builtin_amdgcn_sched_barrier(0);
-    read_frags(next, 0, fwx, fax);  // past the last step: a slot nobody uses
-    mfmas(fwy, fay);
-    sched_pattern<0, NMFMA, NREAD, 0>();
-    __builtin_amdgcn_sched_barrier(0);
+    // second half: after each MFMA, its share of the next step's first-half fragments (past the
+    // last step: a slot nobody uses) and of the refill DMAs of step kt + S into this slot --
+    // issued as one block after the barrier, the DMAs left the MFMAs idle while the four waves
+    // queued them
+    {
+      const int64_t koff = (int64_t)min(kt + S, nk - 1) * KS;
+      uint8_t* dst = lds + slot * SLOT;
+      const uint8_t* src = lds + next * SLOT;
+      const int o0 = ((2 * g) ^ fsw) * 16, o1 = ((2 * g + 1) ^ fsw) * 16;
+      static_for<0, NMFMA>([&](auto qc) {
+        constexpr int Q = decltype(qc)::value, I = Q / FM, J = Q % FM;
+        acc[I][J] = mfma_32x32x64_fp8(fwy[I], fay[J], acc[I][J]);
+        if constexpr (Q < FN + FM) {
+          const uint8_t* r = src + (Q < FN ? w_row0 + Q * 32 * KS : a_row0 + (Q - FN) * 32 * KS);
+          const v4i lo = *(const v4i*)(r + o0);
+          const v4i hi = *(const v4i*)(r + o1);
+          const v8i f = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+          if constexpr (Q < FN) fwx[Q] = f; else fax[Q - FN] = f;
+        }
+        constexpr int LD = (LOADS + NMFMA - 1) / NMFMA;
+#pragma unroll
+        for (int d = Q * LD; d < (Q + 1) * LD && d < LOADS; ++d) {
+          if (d < IA)
+            __builtin_amdgcn_global_load_lds((const void*)(pa[d] + koff), (lds_void*)(dst + (wave * IA + d) * 1024),
+                                             16, 0, 0);
+          else
+            __builtin_amdgcn_global_load_lds((const void*)(pw[d - IA] + koff),
+                                             (lds_void*)(dst + A_BYTES + (wave * IW + d - IA) * 1024), 16, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      static_assert(NMFMA >= FN + FM, "one fragment read per MFMA");
+    }
     slot = next;
   }
   finish_tile<kBf16, kEpi, BM, BN>(acc, job, lds, wave, lane, M, N, sa, sb, bias, C, ldc, res, nullptr);
@@ -1305,7 +1350,7 @@ hipError_t launch_4w(const GemmArgs& g, hipStream_t st) {
                  (int64_t)g.N * g.K <= kLim && ((int64_t)(g.M - 1) * g.ldc + g.N) * 2 <= kLim && P % 8 == 0 &&
                  bulk >= 1 && (kEpi != kEpiResidual || ((int64_t)(g.M - 1) * g.ldr + g.N) * 2 <= kLim);
     if (persistent)
-      hipLaunchKernelGGL((fp8_gemm_4p<kBf16, kEpi>), dim3(bulk < P ? bulk : P), dim3(256), 0, st, (const uint8_t*)g.A,
+      hipLaunchKernelGGL((fp8_gemm_4q<kBf16, kEpi, 256>), dim3(bulk < P ? bulk : P), dim3(256), 0, st, (const uint8_t*)g.A,
                          (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N,
                          g.K, g.ldc, tiles_m, tiles_n, kGroupM, bulk, residual_args(g));
   }
