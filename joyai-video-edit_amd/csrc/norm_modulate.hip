@@ -423,14 +423,15 @@ __global__ __launch_bounds__(64 * kMaxRowWaves) void norm_mod_rows(NormModArgs a
 }
 
 // One wave per row for the model's rows (N = 512 NV: 4096, 5120), broadcast modulation, no affine
-// weights: the row is held in the wave's registers as NV 16-byte vectors per lane, every reduction is
-// a wave shuffle (no LDS round trip, no barrier per row), and 1 + scale and shift live in LDS as
-// fp32, read by every wave of the workgroup. Waves walk rows wave_id, + total waves; the next row's
-// vectors are loaded while the current row is computed. Same arithmetic per element as
+// weights: the row is held in the wave's registers, unpacked to fp32 once (8 NV values per lane),
+// every reduction is a wave shuffle (no LDS round trip, no barrier per row), and 1 + scale and shift
+// live in LDS as fp32, read by every wave of the workgroup. Waves walk rows wave_id, + total waves;
+// the next row's vectors are loaded while the current row is computed. The FP8 pass quantises the
+// row as rounded to the output dtype, kept as fp32 in the same registers. Same arithmetic per element as
 // norm_mod_rows (x - mean, * r, * (1 + scale) + shift, one rounding; the quantiser of the rounded
 // row), the row sums accumulated per lane in element order and then over the lanes.
 template <bool kFp16, int NORM, bool kFp8, bool kDivide, int NV>
-__global__ __launch_bounds__(256) void norm_mod_wave_rows(NormModArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void norm_mod_wave_rows(NormModArgs a) {
   constexpr int N = 512 * NV;
   __shared__ __attribute__((aligned(16))) float sc1_l[N];
   __shared__ __attribute__((aligned(16))) float shf_l[N];
@@ -456,42 +457,43 @@ __global__ __launch_bounds__(256) void norm_mod_wave_rows(NormModArgs a) {
   uint4 nxt[NV];
   if (row < a.M) load_row(row, nxt);
   for (; row < a.M; row += waves) {
-    uint4 xr[NV];
+    // the row unpacked to fp32 once, then the next row's loads issued into the freed vectors
+    float f[NV][8];
 #pragma unroll
-    for (int i = 0; i < NV; ++i) xr[i] = nxt[i];
+    for (int i = 0; i < NV; ++i) unpack8<kFp16>(nxt[i], f[i]);
     if (row + waves < a.M) load_row(row + waves, nxt);
     // row sums: per lane over its NV vectors in element order, then over the lanes
-    auto row_total = [&](auto elem) -> float {
-      float part = 0.f;
-#pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        float f[8];
-        // an opaque copy: the compiler re-unpacks the vectors instead of keeping 8 NV floats live
-        asm volatile("" : "+v"(xr[i].x), "+v"(xr[i].y), "+v"(xr[i].z), "+v"(xr[i].w));
-        unpack8<kFp16>(xr[i], f);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) part = elem(part, f[j]);
-      }
-      return wave_sum(part);
-    };
     float mean = 0.f, r;
     if constexpr (NORM == 0) {
-      mean = row_total([](float acc, float v) { return acc + v; }) / (float)N;
-      const float var = row_total([mean](float acc, float v) {
-        const float d = v - mean;
-        return acc + d * d;
-      });
-      r = __builtin_amdgcn_rsqf(var / (float)N + a.eps);
+      float part = 0.f;
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) part += f[i][j];
+      mean = wave_sum(part) / (float)N;
+      part = 0.f;
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float d = f[i][j] - mean;
+          part += d * d;
+        }
+      r = __builtin_amdgcn_rsqf(wave_sum(part) / (float)N + a.eps);
     } else {
-      r = __builtin_amdgcn_rsqf(row_total([](float acc, float v) { return acc + v * v; }) / (float)N + a.eps);
+      float part = 0.f;
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) part += f[i][j] * f[i][j];
+      r = __builtin_amdgcn_rsqf(wave_sum(part) / (float)N + a.eps);
     }
-    uint4 y[NV];
     uint32_t amax = 0;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-      float f[8];
-      asm volatile("" : "+v"(xr[i].x), "+v"(xr[i].y), "+v"(xr[i].z), "+v"(xr[i].w));
-      unpack8<kFp16>(xr[i], f);
+      // one vector's modulation operands at a time (hoisting every vector's LDS reads to the top
+      // holds 16 NV more registers)
+      asm volatile("" ::: "memory");
       const int e0 = (lane + 64 * i) * 8;
       const float4 c0 = *(const float4*)&sc1_l[e0], c1 = *(const float4*)&sc1_l[e0 + 4];
       const float4 h0 = *(const float4*)&shf_l[e0], h1 = *(const float4*)&shf_l[e0 + 4];
@@ -500,13 +502,16 @@ __global__ __launch_bounds__(256) void norm_mod_wave_rows(NormModArgs a) {
       float o[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float n = NORM == 0 ? (f[j] - mean) * r : f[j] * r;
+        const float n = NORM == 0 ? (f[i][j] - mean) * r : f[i][j] * r;
         o[j] = n * cs[j] + hs[j];
       }
-      y[i] = make_uint4(pack2<kFp16>(o[0], o[1]), pack2<kFp16>(o[2], o[3]), pack2<kFp16>(o[4], o[5]),
-                        pack2<kFp16>(o[6], o[7]));
-      if (a.out) nt_store16((uint4*)((uint16_t*)a.out + row * N) + lane + 64 * i, y[i]);
-      if constexpr (kFp8) amax = absmax8(amax, y[i]);
+      const uint4 y = make_uint4(pack2<kFp16>(o[0], o[1]), pack2<kFp16>(o[2], o[3]), pack2<kFp16>(o[4], o[5]),
+                                 pack2<kFp16>(o[6], o[7]));
+      if (a.out) nt_store16((uint4*)((uint16_t*)a.out + row * N) + lane + 64 * i, y);
+      if constexpr (kFp8) {
+        amax = absmax8(amax, y);
+        unpack8<kFp16>(y, f[i]);  // the rounded row, which the quantiser sees
+      }
     }
     if constexpr (kFp8) {
       amax = (amax & 0xffffu) > (amax >> 16) ? (amax & 0xffffu) : (amax >> 16);
@@ -518,18 +523,17 @@ __global__ __launch_bounds__(256) void norm_mod_wave_rows(NormModArgs a) {
       uint2* dst = (uint2*)((uint8_t*)a.out_q + row * N);
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
-        float f[8];
-        unpack8<kFp16>(y[i], f);
         uint2 o;
         if (finite) {  // no clamp needed (see norm_mod_rows)
+          float q[8];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) f[j] = kDivide ? div_by_scale(f[j], s, rs) : f[j] * rs;
-          o.x = pack_fp8x4(f[0], f[1], f[2], f[3]);
-          o.y = pack_fp8x4(f[4], f[5], f[6], f[7]);
+          for (int j = 0; j < 8; ++j) q[j] = kDivide ? div_by_scale(f[i][j], s, rs) : f[i][j] * rs;
+          o.x = pack_fp8x4(q[0], q[1], q[2], q[3]);
+          o.y = pack_fp8x4(q[4], q[5], q[6], q[7]);
         } else {
           uint32_t bq[8];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) bq[j] = e4m3fn_soft(clamp_fp8(kDivide ? f[j] / s : f[j] * rs));
+          for (int j = 0; j < 8; ++j) bq[j] = e4m3fn_soft(clamp_fp8(kDivide ? f[i][j] / s : f[i][j] * rs));
           o.x = bq[0] | (bq[1] << 8) | (bq[2] << 16) | (bq[3] << 24);
           o.y = bq[4] | (bq[5] << 8) | (bq[6] << 16) | (bq[7] << 24);
         }
