@@ -59,13 +59,14 @@ __device__ __forceinline__ v16f mfma_32x32x64_fp8(const v8i& a, const v8i& b, co
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 
-// GELU, tanh form: 0.5 x (1 + tanh(u)) == x * sigmoid(2u), u = sqrt(2/pi) (x + 0.044715 x^3).
-// exp2 / rcp hardware approximations (~1 ulp fp32) are far below bf16 resolution.
+// GELU, tanh form: 0.5 x (1 + tanh(u)) == x * sigmoid(2u), u = sqrt(2/pi) (x + 0.044715 x^3),
+// with exp(-2u) = exp2(x (c0 + c1 x^2)), c0 = -2 sqrt(2/pi) log2(e), c1 = 0.044715 c0: seven
+// VALU operations per value. exp2 / rcp hardware approximations (~1 ulp fp32) are far below
+// bf16 resolution.
 __device__ __forceinline__ float gelu_tanh(float x) {
-  const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
-  const float k1 = 0.044715f;
-  const float u2 = 2.0f * k0 * __builtin_fmaf(k1 * x, x * x, x);
-  const float e = __builtin_amdgcn_exp2f(-u2 * 1.4426950408889634f);  // exp(-2u)
+  constexpr float c0 = -2.0f * 0.7978845608028654f * 1.4426950408889634f;
+  constexpr float c1 = 0.044715f * c0;
+  const float e = __builtin_amdgcn_exp2f(x * __builtin_fmaf(x * x, c1, c0));  // exp(-2u)
   return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
@@ -1300,6 +1301,26 @@ ResidualArgs residual_args(const GemmArgs& g) {
 }
 
 
+// Layout rules of the persistent kernel fp8_gemm_4q: K steps in pairs of 128 bytes, row scales
+// read 4 at a time, 32-bit buffer offsets for the operands, the output and the residual.
+bool persistent_ok(const GemmArgs& g) {
+  constexpr int64_t kLim = 0x7fffffffLL;
+  return g.K % 256 == 0 && g.K >= 512 && g.M % 4 == 0 && (int64_t)g.M * g.K <= kLim && (int64_t)g.N * g.K <= kLim &&
+         ((int64_t)(g.M - 1) * g.ldc + g.N) * 2 <= kLim &&
+         (!g.residual || ((int64_t)(g.M - 1) * g.ldr + g.N) * 2 <= kLim);
+}
+
+// One round of 256x128 tiles (tm x tn <= CUs), one tile per workgroup. The one-tile kernel's
+// 3-slot ring beats the persistent 16x16x128 kernel here (1560 x 4096 -> 4096: 29.0 vs 30.0 us,
+// 512 x 5120 -> 13824: 34.9 vs 38.9; same-process A/B, bit-identical).
+template <bool kBf16, int kEpi>
+hipError_t launch_one_round_256x128(const GemmArgs& g, int tm, int tn, hipStream_t st) {
+  hipLaunchKernelGGL((fp8_gemm_4h<kBf16, kEpi, 256, 128, 3>), dim3(tm * tn), dim3(256), 0, st, (const uint8_t*)g.A,
+                     (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N,
+                     g.K, g.ldc, tm, tn, 1, 0, -2, residual_args(g));
+  return hipGetLastError();
+}
+
 // Full rounds of 256x256 tiles (one workgroup per CU), then the remaining tiles of
 // the last, partial round split into 4 (128x128) or 2 (256x128) sub-tiles so that
 // more CUs share that round. Both launches go to the same stream; the result does
@@ -1345,10 +1366,7 @@ hipError_t launch_4w(const GemmArgs& g, hipStream_t st) {
   // 3120 x 4096 -> 4096: 53 vs 56, 1560 x 4096 -> 12288: 90 vs 95 with the sub-tile tail)
   bool persistent = false;
   if constexpr (kEpi == kEpiPlain || kEpi == kEpiGelu || kEpi == kEpiResidual) {
-    constexpr int64_t kLim = 0x7fffffffLL;
-    persistent = g.K % 256 == 0 && g.K >= 512 && g.M % 4 == 0 && (int64_t)g.M * g.K <= kLim &&
-                 (int64_t)g.N * g.K <= kLim && ((int64_t)(g.M - 1) * g.ldc + g.N) * 2 <= kLim && P % 8 == 0 &&
-                 bulk >= 1 && (kEpi != kEpiResidual || ((int64_t)(g.M - 1) * g.ldr + g.N) * 2 <= kLim);
+    persistent = persistent_ok(g) && P % 8 == 0 && bulk >= 1;
     if (persistent)
       hipLaunchKernelGGL((fp8_gemm_4q<kBf16, kEpi, 256>), dim3(bulk < P ? bulk : P), dim3(256), 0, st, (const uint8_t*)g.A,
                          (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N,
@@ -1543,12 +1561,7 @@ hipError_t launch_small_m(const GemmArgs& g, hipStream_t st) {
     // deep-K tiles, hipBLASLt 48; x N 13824 with GELU 42 vs 46). With fewer tiles (N 5120)
     // the deep-K plans stay ahead (128x128 tiles: 30.3 vs 28.8 us).
     const int tm = (g.M + 255) / 256, tn = (g.N + 127) / 128, P = device_cus();
-    if (4 * tm * tn >= 3 * P && tm * tn <= P) {
-      hipLaunchKernelGGL((fp8_gemm_4h<kBf16, kEpi, 256, 128, 3>), dim3(tm * tn), dim3(256), 0, st,
-                         (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias,
-                         (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tm, tn, 1, 0, -2, residual_args(g));
-      return hipGetLastError();
-    }
+    if (4 * tm * tn >= 3 * P && tm * tn <= P) return launch_one_round_256x128<kBf16, kEpi>(g, tm, tn, st);
   }
   SmallPlan p = small_plan(g.M, g.N, g.K, true);
   if (p.splits > 1 && (g.workspace == nullptr || g.workspace_bytes < (int64_t)p.splits * g.M * g.N * 4))
@@ -1603,16 +1616,19 @@ hipError_t launch_gemm_t(const GemmArgs& g, hipStream_t st) {
       if (t128 <= P) return launch_deepk<kBf16, kEpi, 128, 128, 128, 3, 3>(g, 1, nullptr, st);
       // 256x128 tiles with 128-byte steps where they fill more CUs than 128x256 (1560 rows: 224
       // tiles against 208; 1560 x 4096 -> 4096 32.3 us vs 34.0, 1560 x 16384 -> 4096 109.7 vs 112.3)
-      if (t256x128 <= P && t256x128 > t128x256) {
-        const int tm = (g.M + 255) / 256, tn = (g.N + 127) / 128;
-        hipLaunchKernelGGL((fp8_gemm_4h<kBf16, kEpi, 256, 128, 3>), dim3(tm * tn), dim3(256), 0, st,
-                           (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias,
-                           (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tm, tn, 1, 0, -2, residual_args(g));
-        return hipGetLastError();
-      }
+      if (t256x128 <= P && t256x128 > t128x256)
+        return launch_one_round_256x128<kBf16, kEpi>(g, (g.M + 255) / 256, (g.N + 127) / 128, st);
       if (t128x256 <= P) return launch_deepk<kBf16, kEpi, 128, 256, 128, 2, 3>(g, 1, nullptr, st);
-      if (t256x192 <= P) {  // 1024 x 4096 -> 12288: 48.9 us vs 52.8 with 64-byte steps
+      if (t256x192 <= P) {
+        // 256x192 tiles filling the CUs (1024 x 4096 -> 12288: 256 tiles): the persistent kernel,
+        // one tile per workgroup (38.9 vs 43.9 us for the one-tile 32x32x64 kernel, bit-identical)
         const int tm = (g.M + 255) / 256, tn = (g.N + 191) / 192;
+        if (persistent_ok(g)) {
+          hipLaunchKernelGGL((fp8_gemm_4q<kBf16, kEpi, 192>), dim3(tm * tn), dim3(256), 0, st, (const uint8_t*)g.A,
+                             (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias, (uint16_t*)g.C, g.M,
+                             g.N, g.K, g.ldc, tm, tn, kGroupM, tm * tn, residual_args(g));
+          return hipGetLastError();
+        }
         hipLaunchKernelGGL((fp8_gemm_4h<kBf16, kEpi, 256, 192, 2>), dim3(tm * tn), dim3(256), 0, st,
                            (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias,
                            (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, tm, tn, 1, 0, -2, residual_args(g));
