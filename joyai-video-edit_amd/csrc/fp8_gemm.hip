@@ -684,7 +684,9 @@ __device__ __forceinline__ void wait_vmcnt_lgkm0() {
 //     than 32x32x64 at the same MFMA density (MI355X, one wave per SIMD, operands in registers:
 //     2.04 vs 1.87 GHz, both 100 % MFMA-busy; re-read from LDS every step: 1.98 vs 1.83 GHz),
 //     i.e. it draws less power per FLOP, and the part runs these GEMMs power-limited. The
-//     accumulated sums are the 32x32x64 kernels' to the bit on every GEMM test.
+//     GEMM tests that compare it with the 32x32x64 kernels find the same bits; on random
+//     M 10800 operands a few FFN-down outputs differ by <= 2 ulp (the MFMAs sum a 128-byte
+//     K step in another order).
 //
 // Tile BM x BN (BM = 256, BN = 128, 192 or 256), 4 waves in 2 x 2, each a 128 x (BN/2)
 // sub-tile = 8 x FN MFMA tiles of 16 x 16 (FN = BN/32; 4 fp32 accumulators each). Operand
