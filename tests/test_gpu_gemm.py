@@ -245,7 +245,8 @@ def test_cfg3_small_m(M, N):
 
 
 def gemm_capi(qa_u8, qw_u8, sa, sw, bias_u16, out_dtype, workspace):
-    """joy_fp8_scaled_mm through the C ABI with an explicit workspace choice."""
+    """joy_fp8_scaled_mm through the C ABI with an explicit workspace choice: True (a fresh
+    uninitialised one of the size the library asks for), False (none) or a uint8 device tensor."""
     import joyomni_ops as jo
     from joyomni_ops import _lib
     M, K = qa_u8.shape
@@ -256,10 +257,14 @@ def gemm_capi(qa_u8, qw_u8, sa, sw, bias_u16, out_dtype, workspace):
     b = torch.from_numpy(bias_u16.view(np.int16)).view(out_dtype).to(DEV)
     out = torch.empty(M, N, dtype=out_dtype, device=DEV)
     ws_bytes = jo._LIB.joy_fp8_scaled_mm_workspace_size(M, N, K)
-    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=DEV) if workspace else None
+    if isinstance(workspace, torch.Tensor):
+        ws = workspace
+        assert ws.numel() >= ws_bytes
+    else:
+        ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=DEV) if workspace else None
     st = jo._LIB.joy_fp8_scaled_mm(a.data_ptr(), w.data_ptr(), sa_d.data_ptr(), sw_d.data_ptr(), b.data_ptr(),
                                    out.data_ptr(), 0 if out_dtype == torch.bfloat16 else 1, M, N, K, 0,
-                                   ws.data_ptr() if ws is not None else None, ws_bytes if workspace else 0,
+                                   ws.data_ptr() if ws is not None else None, ws_bytes if ws is not None else 0,
                                    torch.cuda.current_stream().cuda_stream)
     _lib.check(jo._LIB, st)
     torch.cuda.synchronize()
@@ -295,6 +300,44 @@ def test_small_m_plans_exact_with_and_without_workspace(M, N, K):
     assert np.array_equal(u16(y_ws), exp_bits)
     y_nows, _ = gemm_capi(qa, qw, sa, sw, bias, torch.bfloat16, False)
     assert np.array_equal(u16(y_nows), exp_bits)
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 5120, 5120), (256, 5120, 5120), (512, 5120, 13824), (300, 2056, 1664)])
+def test_split_k_workspace_needs_no_initialisation(M, N, K):
+    """The split-K workspace needs no initialisation: whatever it holds before a call -- random bytes,
+    all ones, what the previous call of this or another shape left, zeros -- every split writes its
+    whole partial-sum tile before the reduction reads it, so exact small integers give the oracle's
+    bits on every call that reuses one workspace."""
+    import joyomni_ops as jo
+    announce("gemm split-K workspace contents", M, N, K)
+    rng = np.random.default_rng(M + 7 * N + K)
+    qa = f32_to_e4m3fn(rng.integers(-8, 9, (M, K)).astype(np.float32))
+    qw = f32_to_e4m3fn(rng.integers(-8, 9, (N, K)).astype(np.float32))
+    sa = (2.0 ** rng.integers(-12, -4, M)).astype(np.float32)
+    sw = (2.0 ** rng.integers(-12, -4, N)).astype(np.float32)
+    bias = f32_to_bf16((rng.integers(-64, 64, N) / 16).astype(np.float32))
+    exp_bits, _ = og.scaled_mm(qa, qw, sa, sw, bias)
+    need = jo._LIB.joy_fp8_scaled_mm_workspace_size(M, N, K)
+    assert need > 0, "shape expected to use a K split"
+    other = (64, 5120, 5120) if (M, N, K) != (64, 5120, 5120) else (256, 5120, 5120)
+    need_other = jo._LIB.joy_fp8_scaled_mm_workspace_size(*other)
+    ws = torch.empty(max(need, need_other), dtype=torch.uint8, device=DEV)
+    fills = [("random bytes", lambda: ws.copy_(torch.randint(0, 256, ws.shape, dtype=torch.uint8, device=DEV))),
+             ("all ones", lambda: ws.fill_(255)),
+             ("as the previous call left it", lambda: None),
+             ("after another shape's call", None),
+             ("zeros", lambda: ws.zero_())]
+    for name, fill in fills:
+        if fill is None:
+            oa, ow = (f32_to_e4m3fn(rng.integers(-8, 9, (other[0], other[2])).astype(np.float32)),
+                      f32_to_e4m3fn(rng.integers(-8, 9, (other[1], other[2])).astype(np.float32)))
+            gemm_capi(oa, ow, np.ones(other[0], np.float32), np.ones(other[1], np.float32),
+                      np.zeros(other[1], np.uint16), torch.bfloat16, ws)
+        else:
+            fill()
+        torch.cuda.synchronize()
+        y, _ = gemm_capi(qa, qw, sa, sw, bias, torch.bfloat16, ws)
+        assert np.array_equal(u16(y), exp_bits), name
 
 
 @pytest.mark.parametrize("M,N,K", [(64, 5120, 5120), (256, 5120, 5120), (512, 5120, 13824)])
