@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define JOY_ABI_VERSION 9
+#define JOY_ABI_VERSION 10
 
 #if defined(__GNUC__) || defined(__clang__)
 #define JOY_API __attribute__((visibility("default")))
@@ -203,6 +203,36 @@ JOY_API joy_status joy_fused_qkv_norm_rope_cache(const void *qkv, int64_t qkv_ro
                                          void *cache_k, void *cache_v, int64_t num_slots,
                                          int64_t slot_capacity, int64_t slot, int64_t slot_offset,
                                          int64_t cache_tokens, int cache_post_rope, void *stream);
+
+/*
+ * The QKV projection and joy_fused_qkv_norm_rope_cache in one call (new op, no single
+ * reference counterpart): the image stream's QKV Fp8Linear (deploy/xvideo/models/dit/dit.py:409,
+ * fp8_linear.py:114-141 on quantised activations) followed by the split, q/k RMSNorm, RoPE and
+ * ring write of dit.py:409-451 -- joy_fp8_scaled_mm (bf16 out, [M, 3*num_heads*head_dim]) then
+ * joy_fused_qkv_norm_rope_cache with seq_len = M and qkv its output, with the same results bit
+ * for bit. Where the shape allows (head_dim 128, an even num_heads, K % 256 == 0, 32-bit
+ * offsets) the GEMM's epilogue does the norm, rotation and writes itself, so the QKV rows never
+ * reach HBM; the tiles of a last, partial round (and other shapes entirely) go through
+ * `scratch` (bf16 [M, 3*num_heads*head_dim]) and the standalone kernel.
+ * GEMM arguments as joy_fp8_scaled_mm (mat_b: [3*num_heads*head_dim, K] e4m3fn, bias bf16 or
+ * NULL); norm/RoPE/ring arguments as joy_fused_qkv_norm_rope_cache (cos/sin [M, head_dim/2]).
+ * scratch: 16-byte aligned device memory of at least joy_fp8_qkv_norm_rope_cache_scratch_size
+ * bytes (may be NULL when that is 0).
+ */
+JOY_API joy_status joy_fp8_qkv_norm_rope_cache(const void *mat_a, const void *mat_b, const float *scales_a,
+                                               const float *scales_b, const void *bias, int64_t M, int64_t K,
+                                               int64_t num_heads, int64_t head_dim, float eps,
+                                               const void *q_weight, const void *k_weight, const void *cos,
+                                               const void *sin, void *q_out, int64_t q_out_stride, void *k_out,
+                                               int64_t k_out_stride, void *v_out, int64_t v_out_stride,
+                                               void *cache_k, void *cache_v, int64_t num_slots,
+                                               int64_t slot_capacity, int64_t slot, int64_t slot_offset,
+                                               int64_t cache_tokens, int cache_post_rope, void *scratch,
+                                               int64_t scratch_bytes, void *stream);
+
+/* Bytes of scratch joy_fp8_qkv_norm_rope_cache needs (0 when every tile takes the fused epilogue). */
+JOY_API int64_t joy_fp8_qkv_norm_rope_cache_scratch_size(int64_t M, int64_t K, int64_t num_heads,
+                                                         int64_t head_dim);
 
 /*
  * A bf16 [len, num_heads, head_dim] view with a dense last dimension: element

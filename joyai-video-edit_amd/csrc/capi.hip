@@ -36,10 +36,13 @@ bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 // The norm/RoPE kernel indexes (token, head) units with 32-bit integers.
 constexpr int64_t kMaxUnits = 0x7ff00000LL;
 
-joy_status scaled_mm_common(const void* mat_a, const void* mat_b, const float* scales_a, const float* scales_b,
-                            const void* bias, void* out, int out_dtype, int64_t M, int64_t N, int64_t K,
-                            int epilogue, const void* residual, int64_t residual_stride, const void* gate,
-                            void* workspace, int64_t workspace_bytes, void* stream) {
+// Argument rules of the GEMM entry points; fills g. *empty: nothing to launch (M or N is 0).
+// out_optional: out may be null (the fused QKV projection's scratch when no tile needs it).
+joy_status gemm_args(const void* mat_a, const void* mat_b, const float* scales_a, const float* scales_b,
+                     const void* bias, void* out, int out_dtype, int64_t M, int64_t N, int64_t K, int epilogue,
+                     const void* residual, int64_t residual_stride, const void* gate, void* workspace,
+                     int64_t workspace_bytes, bool out_optional, joy::GemmArgs& g, bool* empty) {
+  *empty = false;
   if (M < 0 || N < 0 || K < 0) return fail(JOY_ERR_INVALID_ARGUMENT, "mat_a and mat_b shapes cannot be multiplied");
   if (K % 16 != 0)
     return fail(JOY_ERR_INVALID_ARGUMENT, "mat_a must be multiple of 16 bytes for memory alignment");
@@ -59,14 +62,17 @@ joy_status scaled_mm_common(const void* mat_a, const void* mat_b, const float* s
     return fail(JOY_ERR_INVALID_ARGUMENT, "workspace_bytes must be >= 0, with a workspace when > 0");
   if (workspace && !aligned(workspace, 16))
     return fail(JOY_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
-  if (M == 0 || N == 0) return ok();
-  if (!out || !scales_a || !scales_b || (K > 0 && (!mat_a || !mat_b)))
+  if (M == 0 || N == 0) {
+    *empty = true;
+    return ok();
+  }
+  if ((!out && !out_optional) || !scales_a || !scales_b || (K > 0 && (!mat_a || !mat_b)))
     return fail(JOY_ERR_INVALID_ARGUMENT, "mat_a, mat_b, scales and out must be non-null");
   if (!aligned(mat_a, 16) || !aligned(mat_b, 16) || !aligned(out, 16) || !aligned(scales_b, 16))
     return fail(JOY_ERR_UNSUPPORTED, "mat_a, mat_b, out and scales_b must be 16-byte aligned");
   if (!aligned(scales_a, 4) || (bias && !aligned(bias, 2)) || (residual && (!aligned(residual, 2) || !aligned(gate, 2))))
     return fail(JOY_ERR_INVALID_ARGUMENT, "scales_a, bias, residual and gate must be naturally aligned");
-  joy::GemmArgs g;
+  g = joy::GemmArgs{};
   g.A = mat_a;
   g.W = mat_b;
   g.scales_a = scales_a;
@@ -85,6 +91,18 @@ joy_status scaled_mm_common(const void* mat_a, const void* mat_b, const float* s
   g.gate = gate;
   g.workspace = workspace;
   g.workspace_bytes = workspace ? workspace_bytes : 0;
+  return ok();
+}
+
+joy_status scaled_mm_common(const void* mat_a, const void* mat_b, const float* scales_a, const float* scales_b,
+                            const void* bias, void* out, int out_dtype, int64_t M, int64_t N, int64_t K,
+                            int epilogue, const void* residual, int64_t residual_stride, const void* gate,
+                            void* workspace, int64_t workspace_bytes, void* stream) {
+  joy::GemmArgs g;
+  bool empty;
+  const joy_status st = gemm_args(mat_a, mat_b, scales_a, scales_b, bias, out, out_dtype, M, N, K, epilogue, residual,
+                                  residual_stride, gate, workspace, workspace_bytes, false, g, &empty);
+  if (st != JOY_OK || empty) return st;
   return hip_status(joy::launch_fp8_gemm(g, (hipStream_t)stream),
                     residual ? "fp8_scaled_mm_gated_residual launch" : "fp8_scaled_mm launch");
 }
@@ -122,6 +140,87 @@ joy_status scratch_for_current_device(void** out) {
   *out = g_scratch_ptr[dev];
   return JOY_OK;
 }
+
+// Argument rules of the fused norm/RoPE/ring ops; fills a. With qkv == nullptr (the fused QKV
+// projection, whose GEMM makes the input) the input checks are skipped and a's inputs stay
+// null. *empty: nothing to launch.
+joy_status norm_rope_args(const void* qkv, int64_t qkv_row_stride, int64_t seq_len, int64_t num_heads,
+                          int64_t head_dim, float eps, const void* q_weight, const void* k_weight, const void* cos,
+                          const void* sin, void* q_out, int64_t q_out_stride, void* k_out, int64_t k_out_stride,
+                          void* v_out, int64_t v_out_stride, void* cache_k, void* cache_v, int64_t num_slots,
+                          int64_t slot_capacity, int64_t slot, int64_t slot_offset, int64_t cache_tokens,
+                          int cache_post_rope, joy::NormRopeArgs& a, bool* empty) {
+  *empty = false;
+  if (seq_len < 0 || num_heads < 0) return fail(JOY_ERR_INVALID_ARGUMENT, "seq_len and num_heads must be >= 0");
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "Unsupported head_dim: %lld", (long long)head_dim);
+  if (num_heads > 0x7fffffffLL) return fail(JOY_ERR_UNSUPPORTED, "num_heads too large");
+  const int64_t E = num_heads * head_dim;
+  if (qkv && qkv_row_stride < 3 * E) return fail(JOY_ERR_INVALID_ARGUMENT, "qkv row stride must be >= 3*num_heads*head_dim");
+  if ((q_out && q_out_stride < E) || (k_out && k_out_stride < E) || (v_out && v_out_stride < E))
+    return fail(JOY_ERR_INVALID_ARGUMENT, "q_out/k_out/v_out token stride must be >= num_heads*head_dim");
+  if ((cache_k == nullptr) != (cache_v == nullptr))
+    return fail(JOY_ERR_INVALID_ARGUMENT, "cache_k and cache_v must be provided together");
+  if (cache_k) {
+    if (num_slots <= 0 || slot_capacity < 0)
+      return fail(JOY_ERR_INVALID_ARGUMENT, "cache must have num_slots > 0 and slot_capacity >= 0");
+    if (slot < 0 || slot >= num_slots)
+      return fail(JOY_ERR_INVALID_ARGUMENT, "slot %lld out of range [0, %lld)", (long long)slot,
+                  (long long)num_slots);
+    if (cache_tokens < 0 || cache_tokens > seq_len)
+      return fail(JOY_ERR_INVALID_ARGUMENT, "cache_tokens %lld out of range [0, seq_len = %lld]",
+                  (long long)cache_tokens, (long long)seq_len);
+    if (slot_offset < 0 || slot_offset + cache_tokens > slot_capacity)
+      return fail(JOY_ERR_INVALID_ARGUMENT, "tokens [%lld, %lld) do not fit a slot of %lld tokens",
+                  (long long)slot_offset, (long long)(slot_offset + cache_tokens), (long long)slot_capacity);
+  }
+  if ((!q_out && !k_out && !v_out && !cache_k) || seq_len == 0 || num_heads == 0) {  // nothing to write
+    *empty = true;
+    return ok();
+  }
+  if (seq_len * num_heads > kMaxUnits)
+    return fail(JOY_ERR_UNSUPPORTED, "seq_len*num_heads above 2^31 - 2^20");
+  if (!q_weight || !k_weight || !cos || !sin)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "qkv, weights and cos/sin must be non-null");
+  if ((qkv && (qkv_row_stride % 8)) || (q_out && (q_out_stride % 8)) || (k_out && (k_out_stride % 8)) ||
+      (v_out && (v_out_stride % 8)))
+    return fail(JOY_ERR_UNSUPPORTED, "token strides must be multiples of 8 elements");
+  if ((qkv && !aligned(qkv, 16)) || (q_out && !aligned(q_out, 16)) || (k_out && !aligned(k_out, 16)) ||
+      (v_out && !aligned(v_out, 16)) ||
+      (cache_k && (!aligned(cache_k, 16) || !aligned(cache_v, 16))) || !aligned(q_weight, 16) ||
+      !aligned(k_weight, 16) || !aligned(cos, 8) || !aligned(sin, 8))
+    return fail(JOY_ERR_UNSUPPORTED, "tensors must be 16-byte aligned (cos/sin 8-byte)");
+  const uint16_t* base = (const uint16_t*)qkv;
+  a = joy::NormRopeArgs{};
+  a.q_in = q_out && qkv ? base : nullptr;
+  a.k_in = qkv ? base + E : nullptr;
+  a.v_in = (cache_v || v_out) && qkv ? base + 2 * E : nullptr;
+  a.in_stride = qkv_row_stride;
+  a.q_out = (uint16_t*)q_out;
+  a.q_out_stride = q_out_stride;
+  a.k_out = (uint16_t*)k_out;
+  a.k_out_stride = k_out_stride;
+  const int64_t slot_base = cache_k ? (slot * slot_capacity + slot_offset) * E : 0;
+  a.kpre_out = cache_k ? (uint16_t*)cache_k + slot_base : nullptr;
+  a.kpre_stride = E;
+  a.v_out = cache_v ? (uint16_t*)cache_v + slot_base : nullptr;
+  a.v_out_stride = E;
+  a.v_out2 = (uint16_t*)v_out;
+  a.v_out2_stride = v_out_stride;
+  a.q_weight = (const uint16_t*)q_weight;
+  a.k_weight = (const uint16_t*)k_weight;
+  a.cos = (const uint16_t*)cos;
+  a.sin = (const uint16_t*)sin;
+  a.n_tokens = seq_len;
+  a.table_len = seq_len;
+  a.cache_tokens = cache_k ? cache_tokens : 0;
+  a.cache_post_rope = cache_post_rope != 0;
+  a.num_heads = (int)num_heads;
+  a.eps = eps;
+  return ok();
+}
+
+
 
 }  // namespace
 
@@ -268,72 +367,56 @@ joy_status joy_fused_qkv_norm_rope_cache(const void* qkv, int64_t qkv_row_stride
                                          void* cache_k, void* cache_v, int64_t num_slots,
                                          int64_t slot_capacity, int64_t slot, int64_t slot_offset,
                                          int64_t cache_tokens, int cache_post_rope, void* stream) {
-  if (seq_len < 0 || num_heads < 0) return fail(JOY_ERR_INVALID_ARGUMENT, "seq_len and num_heads must be >= 0");
-  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
-    return fail(JOY_ERR_INVALID_ARGUMENT, "Unsupported head_dim: %lld", (long long)head_dim);
-  if (num_heads > 0x7fffffffLL) return fail(JOY_ERR_UNSUPPORTED, "num_heads too large");
-  const int64_t E = num_heads * head_dim;
-  if (qkv_row_stride < 3 * E) return fail(JOY_ERR_INVALID_ARGUMENT, "qkv row stride must be >= 3*num_heads*head_dim");
-  if ((q_out && q_out_stride < E) || (k_out && k_out_stride < E) || (v_out && v_out_stride < E))
-    return fail(JOY_ERR_INVALID_ARGUMENT, "q_out/k_out/v_out token stride must be >= num_heads*head_dim");
-  if ((cache_k == nullptr) != (cache_v == nullptr))
-    return fail(JOY_ERR_INVALID_ARGUMENT, "cache_k and cache_v must be provided together");
-  if (cache_k) {
-    if (num_slots <= 0 || slot_capacity < 0)
-      return fail(JOY_ERR_INVALID_ARGUMENT, "cache must have num_slots > 0 and slot_capacity >= 0");
-    if (slot < 0 || slot >= num_slots)
-      return fail(JOY_ERR_INVALID_ARGUMENT, "slot %lld out of range [0, %lld)", (long long)slot,
-                  (long long)num_slots);
-    if (cache_tokens < 0 || cache_tokens > seq_len)
-      return fail(JOY_ERR_INVALID_ARGUMENT, "cache_tokens %lld out of range [0, seq_len = %lld]",
-                  (long long)cache_tokens, (long long)seq_len);
-    if (slot_offset < 0 || slot_offset + cache_tokens > slot_capacity)
-      return fail(JOY_ERR_INVALID_ARGUMENT, "tokens [%lld, %lld) do not fit a slot of %lld tokens",
-                  (long long)slot_offset, (long long)(slot_offset + cache_tokens), (long long)slot_capacity);
-  }
-  if (!q_out && !k_out && !v_out && !cache_k) return ok();  // nothing to write
-  if (seq_len == 0 || num_heads == 0) return ok();
-  if (seq_len * num_heads > kMaxUnits)
-    return fail(JOY_ERR_UNSUPPORTED, "seq_len*num_heads above 2^31 - 2^20");
-  if (!qkv || !q_weight || !k_weight || !cos || !sin)
-    return fail(JOY_ERR_INVALID_ARGUMENT, "qkv, weights and cos/sin must be non-null");
-  if ((qkv_row_stride % 8) || (q_out && (q_out_stride % 8)) || (k_out && (k_out_stride % 8)) ||
-      (v_out && (v_out_stride % 8)))
-    return fail(JOY_ERR_UNSUPPORTED, "token strides must be multiples of 8 elements");
-  if (!aligned(qkv, 16) || (q_out && !aligned(q_out, 16)) || (k_out && !aligned(k_out, 16)) ||
-      (v_out && !aligned(v_out, 16)) ||
-      (cache_k && (!aligned(cache_k, 16) || !aligned(cache_v, 16))) || !aligned(q_weight, 16) ||
-      !aligned(k_weight, 16) || !aligned(cos, 8) || !aligned(sin, 8))
-    return fail(JOY_ERR_UNSUPPORTED, "tensors must be 16-byte aligned (cos/sin 8-byte)");
-  const uint16_t* base = (const uint16_t*)qkv;
   joy::NormRopeArgs a;
-  a.q_in = q_out ? base : nullptr;
-  a.k_in = base + E;
-  a.v_in = (cache_v || v_out) ? base + 2 * E : nullptr;
-  a.in_stride = qkv_row_stride;
-  a.q_out = (uint16_t*)q_out;
-  a.q_out_stride = q_out_stride;
-  a.k_out = (uint16_t*)k_out;
-  a.k_out_stride = k_out_stride;
-  const int64_t slot_base = cache_k ? (slot * slot_capacity + slot_offset) * E : 0;
-  a.kpre_out = cache_k ? (uint16_t*)cache_k + slot_base : nullptr;
-  a.kpre_stride = E;
-  a.v_out = cache_v ? (uint16_t*)cache_v + slot_base : nullptr;
-  a.v_out_stride = E;
-  a.v_out2 = (uint16_t*)v_out;
-  a.v_out2_stride = v_out_stride;
-  a.q_weight = (const uint16_t*)q_weight;
-  a.k_weight = (const uint16_t*)k_weight;
-  a.cos = (const uint16_t*)cos;
-  a.sin = (const uint16_t*)sin;
-  a.n_tokens = seq_len;
-  a.table_len = seq_len;
-  a.cache_tokens = cache_k ? cache_tokens : 0;
-  a.cache_post_rope = cache_post_rope != 0;
-  a.num_heads = (int)num_heads;
-  a.eps = eps;
+  bool empty;
+  // a null qkv is checked as the fused QKV projection's (no input) and refused below
+  const joy_status st = norm_rope_args(qkv, qkv_row_stride, seq_len, num_heads, head_dim, eps, q_weight, k_weight, cos,
+                                       sin, q_out, q_out_stride, k_out, k_out_stride, v_out, v_out_stride, cache_k,
+                                       cache_v, num_slots, slot_capacity, slot, slot_offset, cache_tokens,
+                                       cache_post_rope, a, &empty);
+  if (st != JOY_OK || empty) return st;
+  if (!qkv) return fail(JOY_ERR_INVALID_ARGUMENT, "qkv, weights and cos/sin must be non-null");
   return hip_status(joy::launch_qk_norm_rope(a, (int)head_dim, (hipStream_t)stream),
                     "fused_qkv_norm_rope_cache launch");
+}
+
+int64_t joy_fp8_qkv_norm_rope_cache_scratch_size(int64_t M, int64_t K, int64_t num_heads, int64_t head_dim) {
+  if (M <= 0 || K <= 0 || num_heads <= 0 || head_dim <= 0 || M > 0x7fffffffLL || K > 0x7fffffffLL ||
+      3 * num_heads * head_dim > 0x7fffffffLL)
+    return 0;
+  return joy::fp8_gemm_qkv_scratch_bytes((int)M, (int)(3 * num_heads * head_dim), (int)K, (int)num_heads,
+                                         (int)head_dim);
+}
+
+joy_status joy_fp8_qkv_norm_rope_cache(const void* mat_a, const void* mat_b, const float* scales_a,
+                                       const float* scales_b, const void* bias, int64_t M, int64_t K,
+                                       int64_t num_heads, int64_t head_dim, float eps, const void* q_weight,
+                                       const void* k_weight, const void* cos, const void* sin, void* q_out,
+                                       int64_t q_out_stride, void* k_out, int64_t k_out_stride, void* v_out,
+                                       int64_t v_out_stride, void* cache_k, void* cache_v, int64_t num_slots,
+                                       int64_t slot_capacity, int64_t slot, int64_t slot_offset,
+                                       int64_t cache_tokens, int cache_post_rope, void* scratch,
+                                       int64_t scratch_bytes, void* stream) {
+  joy::NormRopeArgs a;
+  bool empty_n;
+  joy_status st = norm_rope_args(nullptr, 0, M, num_heads, head_dim, eps, q_weight, k_weight, cos, sin, q_out,
+                                 q_out_stride, k_out, k_out_stride, v_out, v_out_stride, cache_k, cache_v, num_slots,
+                                 slot_capacity, slot, slot_offset, cache_tokens, cache_post_rope, a, &empty_n);
+  if (st != JOY_OK) return st;
+  const int64_t N = 3 * num_heads * head_dim;
+  if (scratch_bytes < 0 || (scratch_bytes > 0 && !scratch))
+    return fail(JOY_ERR_INVALID_ARGUMENT, "scratch_bytes must be >= 0, with a scratch buffer when > 0");
+  const int64_t need = joy_fp8_qkv_norm_rope_cache_scratch_size(M, K, num_heads, head_dim);
+  if (scratch_bytes < need)
+    return fail(JOY_ERR_INVALID_ARGUMENT, "fp8_qkv_norm_rope_cache: %lld bytes of scratch needed, %lld given",
+                (long long)need, (long long)scratch_bytes);
+  joy::GemmArgs g;
+  bool empty_g;
+  st = gemm_args(mat_a, mat_b, scales_a, scales_b, bias, scratch, JOY_DTYPE_BF16, M, N, K, JOY_EPILOGUE_NONE, nullptr,
+                 0, nullptr, nullptr, 0, true, g, &empty_g);
+  if (st != JOY_OK || empty_n || empty_g) return st;
+  return hip_status(joy::launch_fp8_gemm_qkv(g, a, (int)head_dim, (hipStream_t)stream),
+                    "fp8_qkv_norm_rope_cache launch");
 }
 
 }  // extern "C"

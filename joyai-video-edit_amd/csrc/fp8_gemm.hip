@@ -125,8 +125,28 @@ struct ResidualArgs {
 
 // Epilogue kinds, a template parameter so that the plain and GELU kernels carry no
 // residual registers. kEpiPartial writes the raw fp32 accumulators of a K range
-// (split-K) to a workspace; the reduce kernel applies one of the other kinds.
-enum Epi : int { kEpiPlain = 0, kEpiGelu = 1, kEpiResidual = 2, kEpiPartial = 3 };
+// (split-K) to a workspace; the reduce kernel applies one of the other kinds. kEpiQkv
+// (persistent kernel only): the QKV projection's q/k RMSNorm, RoPE and KV-ring write on
+// the rounded tile instead of storing it (QkvEpi).
+enum Epi : int { kEpiPlain = 0, kEpiGelu = 1, kEpiResidual = 2, kEpiPartial = 3, kEpiQkv = 4 };
+
+// Outputs of the fused QKV epilogue, each a bf16 [rows, heads, 128] view with a token stride
+// (elements): 0 rotated q, 1 rotated k, 2 ring K (normalised, or rotated when kpre_rotated),
+// 3 ring V, 4 a second V (the joint attention V). dst null or rows 0: not written; bytes is
+// the buffer range ((rows - 1) * stride + heads * 128) * 2, so rows past `rows` fall outside.
+struct QkvEpi {
+  uint16_t* dst[5];
+  int64_t stride[5];
+  int bytes[5];
+  int rows[5];
+  const uint16_t* q_weight;  // [128]
+  const uint16_t* k_weight;
+  const uint16_t* cos;  // [M, 64]: token m uses row m
+  const uint16_t* sin;
+  int heads;
+  float eps;
+  bool kpre_rotated;
+};
 
 template <bool kBf16>
 __device__ __forceinline__ uint32_t gated_pair(uint32_t y, uint32_t x, uint32_t g) {
@@ -678,7 +698,8 @@ __device__ __forceinline__ void wait_vmcnt_lgkm0() {
 //     step 2 into side_lds.
 //   * Each wait is a constant count: none of a step's own DMAs may be outstanding when the
 //     next step is read, except in a tile's first step, whose wait (for step 1, fetched during
-//     the previous tile) also counts the NST epilogue stores issued after it.
+//     the previous tile) also counts the NST epilogue stores issued after it (2 NST with the
+//     fused QKV epilogue, of which the wait leaves 63).
 //   * MFMA: v_mfma_scale_f32_16x16x128_f8f6f4, 16 x 16 tiles that each consume a whole
 //     128-byte K step. On random e4m3 operands this instruction sustains a higher shader clock
 //     than 32x32x64 at the same MFMA density (MI355X, one wave per SIMD, operands in registers:
@@ -707,6 +728,19 @@ __device__ __forceinline__ void wait_vmcnt_lgkm0() {
 // cover distinct banks) and stores 16-byte row segments with buffer stores, NSTC per chunk
 // for every wave whatever M and N (out-of-range lanes store past the buffer's range).
 // ---------------------------------------------------------------------------
+// The value of lane ^ 16 without the LDS crossbar: v_permlane16_swap with both operands x
+// gives lane l {x[l & ~16], x[l | 16]}.
+__device__ __forceinline__ float xor16_value(float v, int lane) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((lane & 16) ? r[0] : r[1]);
+}
+// v + (the value of lane ^ 32): v_permlane32_swap with both operands gives {x[l], x[l ^ 32]} in an
+// order that depends on the half; the sum of the two is the same bits in both.
+__device__ __forceinline__ float xor32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ v4f mfma_16x16x128_fp8(const v8i& a, const v8i& b, const v4f& c) {
   // Scale operands of zero select the plain (unscaled) f8f6f4 MFMA; format 0 = e4m3.
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
@@ -716,8 +750,10 @@ template <bool kBf16, int kEpi, int BN>
 __global__ __launch_bounds__(256, 1) void fp8_gemm_4q(
     const uint8_t* __restrict__ A, const uint8_t* __restrict__ W, const float* __restrict__ sa,
     const float* __restrict__ sb, const uint16_t* __restrict__ bias, uint16_t* __restrict__ C,
-    int M, int N, int K, int64_t ldc, int tiles_m, int tiles_n, int group_m, int ntiles, ResidualArgs res) {
-  static_assert(kEpi == kEpiPlain || kEpi == kEpiGelu || kEpi == kEpiResidual, "plain, GELU, gated residual");
+    int M, int N, int K, int64_t ldc, int tiles_m, int tiles_n, int group_m, int ntiles, ResidualArgs res,
+    QkvEpi qe) {
+  static_assert(kEpi == kEpiPlain || kEpi == kEpiGelu || kEpi == kEpiResidual || kEpi == kEpiQkv, "epilogues");
+  static_assert(kEpi != kEpiQkv || (BN == 256 && kBf16), "fused QKV epilogue: 256-wide tiles (one head per wave), bf16");
   static_assert(BN == 128 || BN == 192 || BN == 256, "tile widths");
   constexpr int BM = 256, KS = 128, NW = 4, S = 2;
   constexpr int WTM = BM / 2, WTN = BN / 2, FM = WTM / 16, FN = WTN / 16, FH = FN / 2;
@@ -735,11 +771,20 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4q(
   __shared__ __attribute__((aligned(1024))) uint8_t lds[S * SLOT];
   __shared__ __attribute__((aligned(1024))) uint8_t side_lds[4096];
   __shared__ __attribute__((aligned(16))) uint8_t stage_lds[NW * STAGE];
+  __shared__ __attribute__((aligned(16))) uint16_t w_lds[kEpi == kEpiQkv ? 256 : 8];  // q then k norm weights
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   const int frow = lane & 15, g = lane >> 4;
+  if constexpr (kEpi == kEpiQkv) {
+    // before the first DMA, so that the wait for these loads counts nothing else
+    if (threadIdx.x < 32) {
+      const uint16_t* src = threadIdx.x < 16 ? qe.q_weight + threadIdx.x * 8 : qe.k_weight + (threadIdx.x - 16) * 8;
+      *(uint4*)(w_lds + threadIdx.x * 8) = *(const uint4*)src;
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the prologue's barrier publishes them
+  }
   const int fsw = swz_rows<KS>(frow);
   // fragment byte offsets of the lane's two 16-byte chunks (logical chunks 2g, 2g + 1; the
   // swizzle is invariant under row -> row + 16)
@@ -872,7 +917,9 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4q(
     if (first) {
       step(IC<0>{}, T_{}, IC<0>{}, true, 2 * KS, T_{});
     } else {
-      step(IC<0>{}, T_{}, IC<NST>{}, true, 2 * KS, T_{});
+      // the fused QKV epilogue issues 2 NST stores (and, on q / k tiles, table loads that it has
+      // waited for) after step 1's last DMA: up to 63 of them may still be in flight
+      step(IC<0>{}, T_{}, IC<kEpi == kEpiQkv ? 63 : NST>{}, true, 2 * KS, T_{});
     }
     first = false;
     step(IC<1>{}, F{}, IC<0>{}, false, 3 * KS, T_{});
@@ -908,6 +955,139 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4q(
       uint8_t* stage = stage_lds + wave * STAGE;
       const int mw = tm0 + wm * WTM, nw0 = tn0 + wn * WTN;
       typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+      if constexpr (kEpi == kEpiQkv) {
+        // this wave's 128 columns are one head of q, k or v (the three blocks are 256-aligned)
+        const int eh = qe.heads * 128, region = tn0 / eh, head = (nw0 - region * eh) >> 7;
+        // the two outputs of the tile: q (rotated q, -), k (rotated k, ring K), v (ring V, joint V)
+        const int o1 = region == 0 ? 0 : (region == 1 ? 1 : 3), o2 = region == 1 ? 2 : 4;
+        const __amdgpu_buffer_rsrc_t rs1 = __builtin_amdgcn_make_buffer_rsrc(qe.dst[o1], 0, qe.bytes[o1], 0x00020000);
+        const __amdgpu_buffer_rsrc_t rs2 =
+            __builtin_amdgcn_make_buffer_rsrc(qe.dst[o2], 0, region == 0 ? 0 : qe.bytes[o2], 0x00020000);
+        const int64_t st1 = qe.stride[o1], st2 = qe.stride[o2];
+        const uint16_t* w_l = w_lds + (region == 1 ? 128 : 0);
+        // rows of the chunk staged through LDS, then stored as 16-byte row segments (NSTC per
+        // lane, for every output and every wave: rows past the output's range fall outside it)
+        auto stage_store = [&](const uint2 (&v)[FN], const __amdgpu_buffer_rsrc_t& rs, int64_t stride, int j) {
+          uint8_t* srow = stage + er * PITCH + eg * 8;
+#pragma unroll
+          for (int i = 0; i < FN; ++i) *(uint2*)(srow + i * 32) = v[i];
+          asm volatile("" ::: "memory");
+#pragma unroll
+          for (int k = 0; k < NSTC; ++k) {
+            const int idx = k * 64 + lane_e, r = idx / CPL, c = idx % CPL;
+            const uint4 x = *(const uint4*)(stage + r * PITCH + c * 16);
+            const int m = mw + j * 16 + r;
+            const uint32_t off =
+                m < M ? (uint32_t)(((int64_t)m * stride + head * 128 + c * 8) * 2) : 0x80000000u;
+            __builtin_amdgcn_raw_buffer_store_b128((u32x4){x.x, x.y, x.z, x.w}, rs, (int)off, 0, 2);
+          }
+          asm volatile("" ::: "memory");
+        };
+        // RoPE tables of chunk j: the cos and sin rows (128 bytes) of its 16 tokens, 16 bytes per
+        // lane and load (lane l: piece l & 7 of row (l >> 3) + 8 (k & 1) of table k >> 1), loaded one
+        // chunk ahead (vmcnt is in order: loads issued after the previous chunk's stores would wait
+        // for them too), then passed through the staging area (rows of 136 bytes: the lanes' 4-byte
+        // reads of one pair column hit distinct banks) to the lanes that rotate each pair
+        u32x4 tb[4], tbn[4];
+        auto load_tables = [&](int j, u32x4 (&t)[4]) {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const int tok = min(mw + j * 16 + (lane_e >> 3) + 8 * (k & 1), M - 1);
+            t[k] = *(const u32x4*)(((k >> 1) ? qe.sin : qe.cos) + (int64_t)tok * 64 + (lane_e & 7) * 8);
+          }
+        };
+        if (region < 2) load_tables(0, tb);
+#pragma unroll
+        for (int j = 0; j < FM; ++j) {
+          int jz;  // re-read the column operands per chunk rather than holding them in registers
+          asm volatile("v_mov_b32 %0, 0" : "=v"(jz));
+          if (region < 2 && j + 1 < FM) load_tables(j + 1, tbn);
+          // the GEMM's rounded output (as the plain epilogue stores it)
+          const float s_a = sa_l[wm * WTM + j * 16 + er];
+          uint2 yb[FN];
+#pragma unroll
+          for (int i = 0; i < FN; ++i) {
+            const int c = wn * WTN + i * 16 + eg * 4;
+            const float4 sv = *(const float4*)(sb_l + c + jz);
+            const uint2 bb = *(const uint2*)(bias_l + c + jz);
+            const float sbe[4] = {sv.x, sv.y, sv.z, sv.w};
+            const float be[4] = {has_bias ? bf16_lo(bb.x) : 0.0f, has_bias ? bf16_hi(bb.x) : 0.0f,
+                                 has_bias ? bf16_lo(bb.y) : 0.0f, has_bias ? bf16_hi(bb.y) : 0.0f};
+            float o[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = __builtin_fmaf(acc[i][j][e] * sbe[e], s_a, be[e]);
+            yb[i] = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+          }
+          if (region == 2) {
+            stage_store(yb, rs1, st1, j);
+            stage_store(yb, rs2, st2, j);
+            continue;
+          }
+          // the lane's 16 pairs i * 8 + eg * 2 and + 1 (i < FN) of token er
+          uint32_t cw[FN], sw[FN];
+          {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              uint8_t* d = stage + ((k >> 1) * 16 + (lane_e >> 3) + 8 * (k & 1)) * 136 + (lane_e & 7) * 16;
+              *(uint2*)d = make_uint2(tb[k][0], tb[k][1]);
+              *(uint2*)(d + 8) = make_uint2(tb[k][2], tb[k][3]);
+            }
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int i = 0; i < FN; ++i) {
+              cw[i] = *(const uint32_t*)(stage + er * 136 + (i * 8 + eg * 2) * 2);
+              sw[i] = *(const uint32_t*)(stage + (16 + er) * 136 + (i * 8 + eg * 2) * 2);
+            }
+            asm volatile("" ::: "memory");
+          }
+          // head RMSNorm: lane (er, eg) holds elements i * 16 + eg * 4 + e of token er's head, so
+          // element group 2 i + (eg >> 1) (8 elements) is split over lanes eg and eg ^ 1: the even
+          // lane's 4-term fma chain continues in the odd lane, whose 8 group sums then take the
+          // tree g ^ 8 (i ^ 4), g ^ 4 (i ^ 2), g ^ 2 (i ^ 1) in the lane and g ^ 1 across lanes
+          // eg and eg ^ 2 -- the order of the standalone kernel (head_rsqrt)
+          float yv[FN][4], s8[FN];
+#pragma unroll
+          for (int i = 0; i < FN; ++i) {
+            yv[i][0] = bf16_lo(yb[i].x);
+            yv[i][1] = bf16_hi(yb[i].x);
+            yv[i][2] = bf16_lo(yb[i].y);
+            yv[i][3] = bf16_hi(yb[i].y);
+            float c4 = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) c4 = __builtin_fmaf(yv[i][e], yv[i][e], c4);
+            float t = xor16_value(c4, lane_e);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) t = __builtin_fmaf(yv[i][e], yv[i][e], t);
+            s8[i] = t;
+          }
+          const float l10 = s8[0] + s8[4], l11 = s8[1] + s8[5], l12 = s8[2] + s8[6], l13 = s8[3] + s8[7];
+          const float l3 = (l10 + l12) + (l11 + l13);
+          const float l4 = xor32_sum(l3);
+          const float l4p = xor16_value(l4, lane_e);
+          const float r = head_rsqrt((eg & 1) ? l4 : l4p, 1.0f / 128.0f, qe.eps);
+          float xh[FN][4];
+          uint2 kb[FN], ob[FN];
+#pragma unroll
+          for (int i = 0; i < FN; ++i) {
+            const uint2 wv = *(const uint2*)(w_l + i * 16 + eg * 4 + jz);
+            const float w[4] = {bf16_lo(wv.x), bf16_hi(wv.x), bf16_lo(wv.y), bf16_hi(wv.y)};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xh[i][e] = yv[i][e] * r * w[e];
+            kb[i] = make_uint2(pack_bf16x2(xh[i][0], xh[i][1]), pack_bf16x2(xh[i][2], xh[i][3]));
+            float ro[4];
+            rope_pair(xh[i][0], xh[i][1], bf16_lo(cw[i]), bf16_lo(sw[i]), ro[0], ro[1]);
+            rope_pair(xh[i][2], xh[i][3], bf16_hi(cw[i]), bf16_hi(sw[i]), ro[2], ro[3]);
+            ob[i] = make_uint2(pack_bf16x2(ro[0], ro[1]), pack_bf16x2(ro[2], ro[3]));
+          }
+          stage_store(ob, rs1, st1, j);
+          if (region == 1 && !qe.kpre_rotated)
+            stage_store(kb, rs2, st2, j);
+          else
+            stage_store(ob, rs2, st2, j);  // q: a range of 0 bytes (nothing stored, same count)
+#pragma unroll
+          for (int k = 0; k < 4; ++k) tb[k] = tbn[k];
+        }
+      } else {
       // the gate of the 8 output columns each lane stores in read-back instruction k (fixed per tile)
       u32x4 gv[NSTC];
 #pragma unroll
@@ -972,6 +1152,7 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4q(
           __builtin_amdgcn_raw_buffer_store_b128((u32x4){v.x, v.y, v.z, v.w}, crs, (int)off, 0, 2);
         }
         asm volatile("" ::: "memory");
+      }
       }
     }
     if (!more) break;
@@ -1372,7 +1553,7 @@ hipError_t launch_4w(const GemmArgs& g, hipStream_t st) {
     if (persistent)
       hipLaunchKernelGGL((fp8_gemm_4q<kBf16, kEpi, 256>), dim3(bulk < P ? bulk : P), dim3(256), 0, st, (const uint8_t*)g.A,
                          (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N,
-                         g.K, g.ldc, tiles_m, tiles_n, kGroupM, bulk, residual_args(g));
+                         g.K, g.ldc, tiles_m, tiles_n, kGroupM, bulk, residual_args(g), QkvEpi{});
   }
   if (bulk > 0 && !persistent) {
     auto kern = fp8_gemm_4w<kBf16, kEpi, 256, 256, D>;
@@ -1628,7 +1809,7 @@ hipError_t launch_gemm_t(const GemmArgs& g, hipStream_t st) {
         if (persistent_ok(g)) {
           hipLaunchKernelGGL((fp8_gemm_4q<kBf16, kEpi, 192>), dim3(tm * tn), dim3(256), 0, st, (const uint8_t*)g.A,
                              (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias, (uint16_t*)g.C, g.M,
-                             g.N, g.K, g.ldc, tm, tn, kGroupM, tm * tn, residual_args(g));
+                             g.N, g.K, g.ldc, tm, tn, kGroupM, tm * tn, residual_args(g), QkvEpi{});
           return hipGetLastError();
         }
         hipLaunchKernelGGL((fp8_gemm_4h<kBf16, kEpi, 256, 192, 2>), dim3(tm * tn), dim3(256), 0, st,
@@ -1648,12 +1829,192 @@ hipError_t launch_gemm_t(const GemmArgs& g, hipStream_t st) {
   return hipGetLastError();
 }
 
+// q/k RMSNorm + RoPE and the KV-ring write of the tiles of a fused QKV projection that the
+// persistent kernel leaves to the sub-tile launch (which stores them plainly in C): one
+// workgroup per sub-tile of BMs rows x one head, 16 lanes per token as in the standalone
+// kernel (same arithmetic order, head_rsqrt), the sub-tile order of fp8_gemm_4h.
+template <int BMs>
+__global__ __launch_bounds__(256) void qkv_tail_norm_rope(const uint16_t* __restrict__ C, int64_t ldc, int M,
+                                                          int tiles_m, int tiles_n, int group_m, int tile_base,
+                                                          int sub_log2, QkvEpi qe) {
+  const TileJob job = decode_job<BMs, 128>(0, tiles_m, tiles_n, group_m, tile_base, sub_log2, 1);
+  const int lane = threadIdx.x & 63, li = lane & 15;
+  const int eh = qe.heads * 128, region = job.n0 / eh, head = (job.n0 - region * eh) >> 7;
+  const int o1 = region == 0 ? 0 : (region == 1 ? 1 : 3), o2 = region == 1 ? 2 : 4;
+  float w[8] = {};
+  if (region < 2) {
+    const uint4 wv = *(const uint4*)((region == 0 ? qe.q_weight : qe.k_weight) + li * 8);
+    const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      w[2 * e] = bf16_lo(ww[e]);
+      w[2 * e + 1] = bf16_hi(ww[e]);
+    }
+  }
+  for (int u0 = 0; u0 < BMs; u0 += 16) {
+    const int m = job.m0 + u0 + (int)(threadIdx.x >> 4);
+    const int mr = min(m, M - 1);  // every lane takes part in the head's shuffles
+    const uint4 x = *(const uint4*)(C + (int64_t)mr * ldc + job.n0 + li * 8);
+    uint4 out1 = x, out2 = x;
+    if (region < 2) {
+      const uint32_t xw[4] = {x.x, x.y, x.z, x.w};
+      float f[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        f[2 * e] = bf16_lo(xw[e]);
+        f[2 * e + 1] = bf16_hi(xw[e]);
+      }
+      float ss = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss = __builtin_fmaf(f[j], f[j], ss);
+#pragma unroll
+      for (int off = 8; off > 0; off >>= 1) ss += __shfl_xor(ss, off, kWave);
+      const float r = head_rsqrt(ss, 1.0f / 128.0f, qe.eps);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) f[j] = f[j] * r * w[j];
+      const uint2 cv = *(const uint2*)(qe.cos + (int64_t)mr * 64 + li * 4);
+      const uint2 sv = *(const uint2*)(qe.sin + (int64_t)mr * 64 + li * 4);
+      const float c[4] = {bf16_lo(cv.x), bf16_hi(cv.x), bf16_lo(cv.y), bf16_hi(cv.y)};
+      const float sn[4] = {bf16_lo(sv.x), bf16_hi(sv.x), bf16_lo(sv.y), bf16_hi(sv.y)};
+      float o[8];
+#pragma unroll
+      for (int p = 0; p < 4; ++p) rope_pair(f[2 * p], f[2 * p + 1], c[p], sn[p], o[2 * p], o[2 * p + 1]);
+      out1 = make_uint4(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]), pack_bf16x2(o[4], o[5]),
+                        pack_bf16x2(o[6], o[7]));
+      out2 = (region == 1 && !qe.kpre_rotated)
+                 ? make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
+                              pack_bf16x2(f[6], f[7]))
+                 : out1;
+    }
+    if (m < M) {
+      if (qe.dst[o1] && m < qe.rows[o1]) *(uint4*)(qe.dst[o1] + (int64_t)m * qe.stride[o1] + head * 128 + li * 8) = out1;
+      if (region > 0 && qe.dst[o2] && m < qe.rows[o2])
+        *(uint4*)(qe.dst[o2] + (int64_t)m * qe.stride[o2] + head * 128 + li * 8) = out2;
+    }
+  }
+}
+
 }  // namespace
 
 int64_t fp8_gemm_workspace_bytes(int M, int N, int K) {
   if (K < 64 || K % 64 != 0 || N % 8 != 0) return 0;
   const SmallPlan p = small_plan(M, N, K, true);
   return p.splits > 1 ? (int64_t)p.splits * M * N * 4 : 0;
+}
+
+namespace {
+// Tile plan of the fused QKV projection: the persistent kernel takes the whole rounds of 256x256
+// tiles (or all tiles when the last round is nearly full), the rest run as 128x128 (sub 2) or
+// 256x128 (sub 1) sub-tiles, as launch_4w splits them.
+struct QkvPlan {
+  int tiles_m, tiles_n, bulk, rem, sub_log2;
+};
+QkvPlan qkv_plan(int M, int N) {
+  QkvPlan p;
+  p.tiles_m = (M + 255) / 256;
+  p.tiles_n = N / 256;
+  const int T = p.tiles_m * p.tiles_n, P = device_cus();
+  p.rem = T % P;
+  p.sub_log2 = 0;
+  if (p.rem * 4 <= P) {
+    p.sub_log2 = 2;
+  } else if (p.rem * 2 <= P + P / 4) {
+    p.sub_log2 = 1;
+  } else {
+    p.rem = 0;
+  }
+  p.bulk = T - p.rem;
+  return p;
+}
+
+bool qkv_fusable(const GemmArgs& g, const NormRopeArgs& a, int head_dim) {
+  const int64_t eh = (int64_t)a.num_heads * 128;
+  if (head_dim != 128 || !g.out_bf16 || g.gelu || g.residual || a.num_heads % 2 != 0 || g.N != 3 * eh) return false;
+  if (a.n_tokens != g.M || a.table_len != g.M || !persistent_ok(g) || device_cus() % 8 != 0) return false;
+  if ((uintptr_t)a.cos % 16 != 0 || (uintptr_t)a.sin % 16 != 0) return false;  // 16-byte table loads
+  const int64_t strides[5] = {a.q_out_stride, a.k_out_stride, a.kpre_stride, a.v_out_stride, a.v_out2_stride};
+  for (int i = 0; i < 5; ++i)
+    if (((int64_t)g.M * strides[i] + eh) * 2 > 0x7fffffffLL) return false;  // 32-bit buffer offsets
+  return true;
+}
+}  // namespace
+
+int64_t fp8_gemm_qkv_scratch_bytes(int M, int N, int K, int num_heads, int head_dim) {
+  if (M <= 0 || N <= 0) return 0;
+  GemmArgs g{};
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.ldc = N;
+  g.out_bf16 = true;
+  NormRopeArgs a{};
+  a.num_heads = num_heads;
+  a.n_tokens = a.table_len = M;
+  a.q_out_stride = a.k_out_stride = a.kpre_stride = a.v_out_stride = a.v_out2_stride = (int64_t)num_heads * head_dim;
+  if (qkv_fusable(g, a, head_dim) && qkv_plan(M, N).rem == 0) return 0;
+  return (int64_t)M * N * 2;
+}
+
+hipError_t launch_fp8_gemm_qkv(const GemmArgs& g, const NormRopeArgs& a, int head_dim, hipStream_t st) {
+  if (g.M == 0 || g.N == 0) return hipSuccess;
+  if (!qkv_fusable(g, a, head_dim) || (qkv_plan(g.M, g.N).rem > 0 && g.C == nullptr)) {
+    // the GEMM into C, then the standalone norm/RoPE kernel on it
+    if (g.C == nullptr) return hipErrorInvalidValue;
+    hipError_t e = launch_fp8_gemm(g, st);
+    if (e != hipSuccess) return e;
+    NormRopeArgs b = a;
+    const uint16_t* c = (const uint16_t*)g.C;
+    const int64_t eh = (int64_t)a.num_heads * head_dim;
+    b.q_in = a.q_out ? c : nullptr;
+    b.k_in = c + eh;
+    b.v_in = (a.v_out || a.v_out2) ? c + 2 * eh : nullptr;
+    b.in_stride = g.ldc;
+    return launch_qk_norm_rope(b, head_dim, st);
+  }
+  QkvEpi qe{};
+  uint16_t* dst[5] = {a.q_out, a.k_out, a.kpre_out, a.v_out, a.v_out2};
+  const int64_t stride[5] = {a.q_out_stride, a.k_out_stride, a.kpre_stride, a.v_out_stride, a.v_out2_stride};
+  const int64_t rows[5] = {g.M, g.M, a.cache_tokens, a.cache_tokens, g.M};
+  for (int i = 0; i < 5; ++i) {
+    const bool on = dst[i] != nullptr && rows[i] > 0;
+    qe.dst[i] = on ? dst[i] : nullptr;
+    qe.stride[i] = stride[i];
+    qe.rows[i] = on ? (int)rows[i] : 0;
+    qe.bytes[i] = on ? (int)(((rows[i] - 1) * stride[i] + (int64_t)a.num_heads * 128) * 2) : 0;
+  }
+  qe.q_weight = a.q_weight;
+  qe.k_weight = a.k_weight;
+  qe.cos = a.cos;
+  qe.sin = a.sin;
+  qe.heads = a.num_heads;
+  qe.eps = a.eps;
+  qe.kpre_rotated = a.cache_post_rope;
+  const QkvPlan p = qkv_plan(g.M, g.N);
+  const int P = device_cus();
+  if (p.bulk > 0) {
+    hipLaunchKernelGGL((fp8_gemm_4q<true, kEpiQkv, 256>), dim3(p.bulk < P ? p.bulk : P), dim3(256), 0, st,
+                       (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias,
+                       (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, p.tiles_m, p.tiles_n, kGroupM, p.bulk, residual_args(g),
+                       qe);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  if (p.rem == 0) return hipSuccess;
+  const uint16_t* c = (const uint16_t*)g.C;
+  if (p.sub_log2 == 2) {
+    hipLaunchKernelGGL((fp8_gemm_4h<true, kEpiPlain, 128, 128, 4>), dim3(p.rem << 2), dim3(256), 0, st,
+                       (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias,
+                       (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, p.tiles_m, p.tiles_n, kGroupM, p.bulk, 2, residual_args(g));
+    hipLaunchKernelGGL((qkv_tail_norm_rope<128>), dim3(p.rem << 2), dim3(256), 0, st, c, g.ldc, g.M, p.tiles_m,
+                       p.tiles_n, kGroupM, p.bulk, 2, qe);
+  } else {
+    hipLaunchKernelGGL((fp8_gemm_4h<true, kEpiPlain, 256, 128, 3>), dim3(p.rem << 1), dim3(256), 0, st,
+                       (const uint8_t*)g.A, (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias,
+                       (uint16_t*)g.C, g.M, g.N, g.K, g.ldc, p.tiles_m, p.tiles_n, kGroupM, p.bulk, 1, residual_args(g));
+    hipLaunchKernelGGL((qkv_tail_norm_rope<256>), dim3(p.rem << 1), dim3(256), 0, st, c, g.ldc, g.M, p.tiles_m,
+                       p.tiles_n, kGroupM, p.bulk, 1, qe);
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_fp8_gemm(const GemmArgs& g, hipStream_t st) {

@@ -119,4 +119,18 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Per-head q/k RMSNorm and rotation (fused_qknorm_rope_3d_kernel.cu:68-105), written with
+// explicit fma so that the standalone norm/RoPE kernel and the QKV GEMM epilogue, which
+// hold a head's elements in different lane layouts, give the same bits. The sum of squares
+// is fma(x_j, x_j, s) over 8 consecutive elements (from 0), then a tree over the head's G =
+// D / 8 groups of 8 (group index = element / 8): g with g ^ (G / 2), then G / 4, ..., 1.
+__device__ __forceinline__ float head_rsqrt(float ss, float inv_d, float eps) {
+  return __builtin_amdgcn_rsqf(__builtin_fmaf(ss, inv_d, eps));
+}
+// pair (x0, x1) rotated by (c, s): (x0 c - x1 s, x0 s + x1 c)
+__device__ __forceinline__ void rope_pair(float x0, float x1, float c, float s, float& o0, float& o1) {
+  o0 = __builtin_fmaf(x0, c, -(x1 * s));
+  o1 = __builtin_fmaf(x0, s, x1 * c);
+}
+
 }  // namespace joy

@@ -120,6 +120,11 @@ hipError_t launch_per_token_quant(const void* in, bool in_fp16, void* q, float* 
                                   int64_t K, bool divide, hipStream_t st);
 hipError_t launch_qk_norm_rope(const NormRopeArgs& a, int head_dim, hipStream_t st);
 hipError_t launch_fp8_gemm(const GemmArgs& g, hipStream_t st);
+// The QKV projection (bf16 [M, 3 * heads * head_dim] = g) with the norm/RoPE/ring outputs of a
+// (its inputs ignored) written by the GEMM's epilogue where the shape allows it; g.C is the
+// scratch for the tiles (or the whole GEMM) that go through the standalone kernel.
+hipError_t launch_fp8_gemm_qkv(const GemmArgs& g, const NormRopeArgs& a, int head_dim, hipStream_t st);
+int64_t fp8_gemm_qkv_scratch_bytes(int M, int N, int K, int num_heads, int head_dim);
 // Workspace bytes the GEMM of this shape can use on the current device (0: none).
 int64_t fp8_gemm_workspace_bytes(int M, int N, int K);
 hipError_t launch_norm_modulate(const NormModArgs& a, hipStream_t st);

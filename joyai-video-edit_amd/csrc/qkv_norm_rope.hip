@@ -61,6 +61,7 @@ __device__ __forceinline__ void st16(uint16_t* p, const uint4& v) {
   }
 }
 
+// the tree over the head's lanes of head_rsqrt's comment: offsets LPH / 2, ..., 1
 template <int LPH>
 __device__ __forceinline__ float head_sum(float v) {
 #pragma unroll
@@ -120,8 +121,8 @@ __global__ __launch_bounds__(512) void qk_norm_rope_kernel(NormRopeArgs a) {
     }
     ssq = head_sum<LPH>(ssq);
     ssk = head_sum<LPH>(ssk);
-    const float rq = __builtin_amdgcn_rsqf(ssq * inv_d + a.eps);
-    const float rk = __builtin_amdgcn_rsqf(ssk * inv_d + a.eps);
+    const float rq = head_rsqrt(ssq, inv_d, a.eps);
+    const float rk = head_rsqrt(ssk, inv_d, a.eps);
     float qo[8], ko[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -130,10 +131,8 @@ __global__ __launch_bounds__(512) void qk_norm_rope_kernel(NormRopeArgs a) {
     }
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
-      qo[2 * p] = q[2 * p] * c[p] - q[2 * p + 1] * s[p];
-      qo[2 * p + 1] = q[2 * p] * s[p] + q[2 * p + 1] * c[p];
-      ko[2 * p] = k[2 * p] * c[p] - k[2 * p + 1] * s[p];
-      ko[2 * p + 1] = k[2 * p] * s[p] + k[2 * p + 1] * c[p];
+      rope_pair(q[2 * p], q[2 * p + 1], c[p], s[p], qo[2 * p], qo[2 * p + 1]);
+      rope_pair(k[2 * p], k[2 * p + 1], c[p], s[p], ko[2 * p], ko[2 * p + 1]);
     }
     if (!valid[r]) continue;
     const int64_t t = token[r];

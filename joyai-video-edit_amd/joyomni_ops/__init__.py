@@ -43,6 +43,7 @@ __all__ = [
     "per_token_quant_fp8",
     "fp8_scaled_mm_gelu_tanh",
     "fused_qkv_norm_rope_cache",
+    "fp8_qkv_norm_rope_cache",
     "fused_norm_scale_shift_fp8",
     "fp8_scaled_mm_gated_residual",
     "fused_cached_kv_pack_out",
@@ -98,6 +99,11 @@ _lib_def.define(
     "Tensor k_weight, Tensor cos, Tensor sin, Tensor(a!)? q_out, Tensor(b!)? k_out, "
     "Tensor(c!)? cache_k, Tensor(d!)? cache_v, int slot, int slot_offset, Tensor(e!)? v_out=None, "
     "int cache_tokens=-1, bool cache_pre_rope=True) -> ()")
+_lib_def.define(
+    "fp8_qkv_norm_rope_cache(Tensor mat_a, Tensor mat_b, Tensor scales_a, Tensor scales_b, Tensor? bias, "
+    "int num_heads, float eps, Tensor q_weight, Tensor k_weight, Tensor cos, Tensor sin, Tensor(a!)? q_out, "
+    "Tensor(b!)? k_out, Tensor(c!)? cache_k, Tensor(d!)? cache_v, int slot, int slot_offset, "
+    "Tensor(e!)? v_out=None, int cache_tokens=-1, bool cache_pre_rope=True) -> ()")
 _lib_def.define(
     "fused_cached_kv_pack_out(Tensor key0, Tensor value0, Tensor? key1, Tensor? value1, "
     "Tensor cos, Tensor sin, Tensor(a!) out_k, Tensor(b!) out_v) -> ()")
@@ -332,6 +338,34 @@ def _token_stride(t: torch.Tensor, L: int, H: int, D: int, name: str, device) ->
     return x.stride(0) if L > 1 else H * D
 
 
+def _norm_rope_out_checks(L, H, D, device, q_weight, k_weight, cos, sin, q_out, k_out, cache_k, cache_v, v_out,
+                          cache_tokens):
+    """Checks of the norm/RoPE/ring outputs shared by fused_qkv_norm_rope_cache and
+    fp8_qkv_norm_rope_cache; returns (token strides of q_out, k_out, v_out, ring slots, slot
+    capacity, cached tokens)."""
+    for name, t in (("q_weight", q_weight), ("k_weight", k_weight), ("cos", cos), ("sin", sin)):
+        _check_input(t, name, torch.bfloat16)
+        _check(t.device == device, f"{name} must be on the device of qkv")
+    _check(q_weight.numel() == D and k_weight.numel() == D, "weight size must match head_dim")
+    _check(cos.shape == (L, D // 2) and sin.shape == (L, D // 2),
+           "cos/sin shape must be [seq_len, head_dim/2]")
+    strides = [_token_stride(t, L, H, D, name, device) if t is not None else 0
+               for name, t in (("q_out", q_out), ("k_out", k_out), ("v_out", v_out))]
+    n_slots = cap = 0
+    if (cache_k is None) != (cache_v is None):
+        raise RuntimeError("cache_k and cache_v must be provided together")
+    n_cache = L if cache_tokens is None or int(cache_tokens) < 0 else int(cache_tokens)
+    if cache_k is not None:
+        for name, t in (("cache_k", cache_k), ("cache_v", cache_v)):
+            _check(t.is_cuda and t.device == device and t.dtype == torch.bfloat16,
+                   f"{name} must be a bf16 CUDA tensor on the device of qkv")
+        _check(cache_k.is_contiguous() and cache_v.is_contiguous(), "cache_k/cache_v must be contiguous")
+        _check(cache_k.dim() == 4 and cache_k.shape == cache_v.shape
+               and cache_k.shape[2:] == (H, D), "cache must be [num_slots, capacity, H, D]")
+        n_slots, cap = cache_k.shape[0], cache_k.shape[1]
+    return strides, n_slots, cap, n_cache
+
+
 @torch.library.impl(_lib_def, "fused_qkv_norm_rope_cache", "CUDA")
 def _fused_qkv_norm_rope_cache_cuda(qkv, num_heads, eps, q_weight, k_weight, cos, sin, q_out,
                                     k_out, cache_k, cache_v, slot, slot_offset, v_out=None, cache_tokens=-1,
@@ -346,32 +380,36 @@ def _fused_qkv_norm_rope_cache_cuda(qkv, num_heads, eps, q_weight, k_weight, cos
     H = int(num_heads)
     _check(H > 0 and E3 % (3 * H) == 0, "qkv width must be 3*num_heads*head_dim")
     D = E3 // (3 * H)
-    for name, t in (("q_weight", q_weight), ("k_weight", k_weight), ("cos", cos), ("sin", sin)):
-        _check_input(t, name, torch.bfloat16)
-        _check(t.device == qkv.device, f"{name} must be on the device of qkv")
-    _check(q_weight.numel() == D and k_weight.numel() == D, "weight size must match head_dim")
-    _check(cos.shape == (L, D // 2) and sin.shape == (L, D // 2),
-           "cos/sin shape must be [seq_len, head_dim/2]")
-    strides = [_token_stride(t, L, H, D, name, qkv.device) if t is not None else 0
-               for name, t in (("q_out", q_out), ("k_out", k_out), ("v_out", v_out))]
-    n_slots = cap = 0
-    if (cache_k is None) != (cache_v is None):
-        raise RuntimeError("cache_k and cache_v must be provided together")
-    n_cache = L if cache_tokens is None or int(cache_tokens) < 0 else int(cache_tokens)
-    if cache_k is not None:
-        for name, t in (("cache_k", cache_k), ("cache_v", cache_v)):
-            _check(t.is_cuda and t.device == qkv.device and t.dtype == torch.bfloat16,
-                   f"{name} must be a bf16 CUDA tensor on the device of qkv")
-        _check(cache_k.is_contiguous() and cache_v.is_contiguous(), "cache_k/cache_v must be contiguous")
-        _check(cache_k.dim() == 4 and cache_k.shape == cache_v.shape
-               and cache_k.shape[2:] == (H, D), "cache must be [num_slots, capacity, H, D]")
-        n_slots, cap = cache_k.shape[0], cache_k.shape[1]
+    strides, n_slots, cap, n_cache = _norm_rope_out_checks(L, H, D, qkv.device, q_weight, k_weight, cos, sin, q_out,
+                                                           k_out, cache_k, cache_v, v_out, cache_tokens)
     with torch.cuda.device(qkv.device):
         st = _LIB.joy_fused_qkv_norm_rope_cache(
             _ptr(x), x.stride(0) if L > 1 else E3, L, H, D, float(eps), _ptr(q_weight), _ptr(k_weight), _ptr(cos),
             _ptr(sin), _ptr(q_out), strides[0], _ptr(k_out), strides[1], _ptr(v_out), strides[2], _ptr(cache_k),
             _ptr(cache_v), n_slots, cap, int(slot), int(slot_offset), n_cache, 0 if cache_pre_rope else 1,
             _stream(qkv))
+    _lib.check(_LIB, st)
+
+
+@torch.library.impl(_lib_def, "fp8_qkv_norm_rope_cache", "CUDA")
+def _fp8_qkv_norm_rope_cache_cuda(mat_a, mat_b, scales_a, scales_b, bias, num_heads, eps, q_weight, k_weight, cos,
+                                  sin, q_out, k_out, cache_k, cache_v, slot, slot_offset, v_out=None,
+                                  cache_tokens=-1, cache_pre_rope=True):
+    M, N, K = _scaled_mm_checks(mat_a, mat_b, scales_a, scales_b, torch.bfloat16, bias)
+    H = int(num_heads)
+    _check(H > 0 and N % (3 * H) == 0, "mat_b width must be 3*num_heads*head_dim")
+    D = N // (3 * H)
+    strides, n_slots, cap, n_cache = _norm_rope_out_checks(M, H, D, mat_a.device, q_weight, k_weight, cos, sin,
+                                                           q_out, k_out, cache_k, cache_v, v_out, cache_tokens)
+    with torch.cuda.device(mat_a.device):
+        nbytes = _LIB.joy_fp8_qkv_norm_rope_cache_scratch_size(M, K, H, D)
+        # the tiles that do not take the fused epilogue pass through this [M, N] bf16 buffer
+        scratch = torch.empty(nbytes, dtype=torch.uint8, device=mat_a.device) if nbytes > 0 else None
+        st = _LIB.joy_fp8_qkv_norm_rope_cache(
+            _ptr(mat_a), _ptr(mat_b), _ptr(scales_a), _ptr(scales_b), _ptr(bias), M, K, H, D, float(eps),
+            _ptr(q_weight), _ptr(k_weight), _ptr(cos), _ptr(sin), _ptr(q_out), strides[0], _ptr(k_out), strides[1],
+            _ptr(v_out), strides[2], _ptr(cache_k), _ptr(cache_v), n_slots, cap, int(slot), int(slot_offset), n_cache,
+            0 if cache_pre_rope else 1, _ptr(scratch), nbytes, _stream(mat_a))
     _lib.check(_LIB, st)
 
 
@@ -725,6 +763,13 @@ def _fake_fused_qkv_norm_rope_cache(qkv, num_heads, eps, q_weight, k_weight, cos
     return None
 
 
+@torch.library.register_fake("joyomni_ops::fp8_qkv_norm_rope_cache")
+def _fake_fp8_qkv_norm_rope_cache(mat_a, mat_b, scales_a, scales_b, bias, num_heads, eps, q_weight, k_weight, cos,
+                                  sin, q_out, k_out, cache_k, cache_v, slot, slot_offset, v_out=None,
+                                  cache_tokens=-1, cache_pre_rope=True):
+    return None
+
+
 @torch.library.register_fake("joyomni_ops::fused_cached_kv_pack_out")
 def _fake_fused_cached_kv_pack_out(key0, value0, key1, value1, cos, sin, out_k, out_v):
     return None
@@ -844,6 +889,18 @@ def fused_qkv_norm_rope_cache(qkv, num_heads, eps, q_weight, k_weight, cos, sin,
     as well, e.g. the video rows of the joint attention V."""
     _ops.fused_qkv_norm_rope_cache(qkv, num_heads, eps, q_weight, k_weight, cos, sin, q_out, k_out,
                                    cache_k, cache_v, slot, slot_offset, v_out, cache_tokens, cache_pre_rope)
+
+
+def fp8_qkv_norm_rope_cache(mat_a, mat_b, scales_a, scales_b, bias, num_heads, eps, q_weight, k_weight, cos, sin,
+                            q_out, k_out=None, cache_k=None, cache_v=None, slot=0, slot_offset=0, v_out=None,
+                            cache_tokens: int = -1, cache_pre_rope: bool = True):
+    """The QKV projection (fp8_scaled_mm to bf16 [M, 3*H*D], scales as there) followed by
+    fused_qkv_norm_rope_cache on its output (same arguments, cos/sin [M, D/2]), with the same
+    results; the GEMM's epilogue writes the norm/RoPE/ring outputs itself where the shape allows,
+    so the QKV rows are not stored in between."""
+    _ops.fp8_qkv_norm_rope_cache(mat_a, mat_b, scales_a, scales_b, bias, num_heads, eps, q_weight, k_weight, cos,
+                                 sin, q_out, k_out, cache_k, cache_v, slot, slot_offset, v_out, cache_tokens,
+                                 cache_pre_rope)
 
 
 def fused_cached_kv_pack_out(key0, value0, key1, value1, cos, sin, out_k, out_v):

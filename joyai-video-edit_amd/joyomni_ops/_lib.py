@@ -61,6 +61,10 @@ SIGNATURES = {
     "joy_fused_qkv_norm_rope_cache": (
         _int, [_vp, _i64, _i64, _i64, _i64, _f32, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _i64,
                _vp, _vp, _i64, _i64, _i64, _i64, _i64, _int, _vp]),
+    "joy_fp8_qkv_norm_rope_cache": (
+        _int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64,
+               _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _int, _vp, _i64, _vp]),
+    "joy_fp8_qkv_norm_rope_cache_scratch_size": (_i64, [_i64, _i64, _i64, _i64]),
     "joy_fused_joint_qkv_pack": (
         _int, [_view, _view, _view, _view, _view, _view, _view, _view, _vp, _vp, _f32, _i64, _i64,
                _vp, _vp, _vp, _vp]),
@@ -76,7 +80,7 @@ SIGNATURES = {
                _vp]),
 }
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 
 class JoyError(RuntimeError):

@@ -52,8 +52,8 @@ from typing import Callable, List, Optional, Sequence, Tuple
 import torch
 import torch.nn as nn
 
-from . import (fused_cached_kv_pack_out, fused_norm_scale_shift_fp8, fused_qkv_norm_rope_cache,
-               fused_text_qkv_pack, sdpa_attention)
+from . import (fp8_qkv_norm_rope_cache, fused_cached_kv_pack_out, fused_norm_scale_shift_fp8,
+               fused_qkv_norm_rope_cache, fused_text_qkv_pack, sdpa_attention)
 from .fp8_linear import Fp8Linear, exact_division_for
 
 NORM_EPS = 1e-6            # dit.py:35
@@ -209,7 +209,7 @@ class QuantizedDoubleStreamBlock:
 
     def __init__(self, hidden: int, heads: int, mlp_hidden: int, device, generator: torch.Generator,
                  quant_rounding: str = "reference_rocm", overlap_streams: bool = True,
-                 attention_backend: str = "hip"):
+                 attention_backend: str = "hip", fuse_qkv: bool = True):
         if attention_backend not in ("hip", "torch_sdpa"):
             raise ValueError(f"attention_backend must be 'hip' or 'torch_sdpa', not {attention_backend!r}")
         # "hip": this library's attention kernel on the token-major joint operands; "torch_sdpa": the
@@ -222,6 +222,10 @@ class QuantizedDoubleStreamBlock:
         # video stream's, between the points where the two streams meet (joint attention operands,
         # attention output); results do not depend on it
         self.overlap_streams = overlap_streams
+        # the video stream's QKV projection and its q/k norm, RoPE and ring write as one op
+        # (fp8_qkv_norm_rope_cache); False: the GEMM, then fused_qkv_norm_rope_cache on its output
+        # (the same bits)
+        self.fuse_qkv = fuse_qkv
         self.img = random_stream_weights(hidden, heads, mlp_hidden, generator, device)
         self.txt = random_stream_weights(hidden, heads, mlp_hidden, generator, device)
         for w in (self.img, self.txt):
@@ -324,6 +328,21 @@ class QuantizedDoubleStreamBlock:
                                      k[:, off:off + n], v[:, off:off + n])
             off, i = off + n, i + len(seg)
 
+    def _video_qkv(self, q8, s8, cos, sin, q_out, k_out, ring_k, ring_v, slot, v_out, n_cache, pre_rope):
+        """The video stream's QKV projection with its q/k RMSNorm, RoPE and ring write
+        (``dit.py:409-451``): fp8_qkv_norm_rope_cache when fused, else the GEMM and then
+        fused_qkv_norm_rope_cache on its output. Returns None (fused) or the QKV rows."""
+        w, H = self.img.qkv, self.heads
+        if self.fuse_qkv:
+            fp8_qkv_norm_rope_cache(q8, w.weight_fp8, s8, w.weight_scale, w.bias, H, NORM_EPS, self.img.q_norm,
+                                    self.img.k_norm, cos, sin, q_out, k_out, ring_k, ring_v, slot, 0, v_out=v_out,
+                                    cache_tokens=n_cache, cache_pre_rope=pre_rope)
+            return None
+        qkv = w.gemm(q8, s8)
+        fused_qkv_norm_rope_cache(qkv, H, NORM_EPS, self.img.q_norm, self.img.k_norm, cos, sin, q_out, k_out, ring_k,
+                                  ring_v, slot, 0, v_out=v_out, cache_tokens=n_cache, cache_pre_rope=pre_rope)
+        return qkv
+
     def forward(self, img: torch.Tensor, txt: torch.Tensor, vec: torch.Tensor, img_cos: torch.Tensor,
                 img_sin: torch.Tensor, ring: Optional[KVRing] = None, write_slot: Optional[int] = None,
                 cached: Sequence[CachedChunk] = (), mark: Optional[Callable[[str], None]] = None,
@@ -355,10 +374,8 @@ class QuantizedDoubleStreamBlock:
         if kv_cache_write_only:
             # only the ring is written: Q is not read, no attention operand is produced
             q8, s8 = self.norm_quant(img2, im[0], im[1], E)
-            img_qkv = self.img.qkv.gemm(q8, s8)
-            fused_qkv_norm_rope_cache(img_qkv, H, NORM_EPS, self.img.q_norm, self.img.k_norm, img_cos, img_sin,
-                                      None, None, ring_k, ring_v, slot, 0, cache_tokens=n_cache,
-                                      cache_pre_rope=kv_cache_pre_rope)
+            self._video_qkv(q8, s8, img_cos, img_sin, None, None, ring_k, ring_v, slot, None, n_cache,
+                            kv_cache_pre_rope)
             ring.lengths[write_slot], ring.pre_rope[write_slot] = n_cache, kv_cache_pre_rope
             ring.touch(write_slot)
             mark("qkv_norm_rope")
@@ -411,17 +428,20 @@ class QuantizedDoubleStreamBlock:
                 tm, txt_qkv = text_qkv()
                 text_pack(txt_qkv)
 
-        # QKV projections
+        # QKV projections; the video stream's q/k norm + RoPE into the joint buffers and K / V into
+        # the ring (in its QKV projection when fused, after it otherwise)
         q8, s8 = self.norm_quant(img2, im[0], im[1], E)
-        img_qkv = self.img.qkv.gemm(q8, s8)
+        args = (img_cos, img_sin, q[0, :L], k[0, C:C + L], ring_k, ring_v, slot, v[0, C:C + L], n_cache,
+                kv_cache_pre_rope)
+        img_qkv = self._video_qkv(q8, s8, *args) if self.fuse_qkv else self.img.qkv.gemm(q8, s8)
         if text and side is None:
             tm, txt_qkv = text_qkv()
         mark("qkv")
 
-        # video q/k norm + RoPE into the joint buffers, K / V into the ring
-        fused_qkv_norm_rope_cache(img_qkv, H, NORM_EPS, self.img.q_norm, self.img.k_norm, img_cos, img_sin,
-                                  q[0, :L], k[0, C:C + L], ring_k, ring_v, slot, 0, v_out=v[0, C:C + L],
-                                  cache_tokens=n_cache, cache_pre_rope=kv_cache_pre_rope)
+        if not self.fuse_qkv:
+            fused_qkv_norm_rope_cache(img_qkv, H, NORM_EPS, self.img.q_norm, self.img.k_norm, img_cos, img_sin,
+                                      q[0, :L], k[0, C:C + L], ring_k, ring_v, slot, 0, v_out=v[0, C:C + L],
+                                      cache_tokens=n_cache, cache_pre_rope=kv_cache_pre_rope)
         if write_slot is not None:
             ring.lengths[write_slot], ring.pre_rope[write_slot] = n_cache, kv_cache_pre_rope
             ring.touch(write_slot)

@@ -414,3 +414,34 @@ def test_block_torch_sdpa_backend_matches_hip_attention():
         assert rms_rel(b, a, base) <= 3e-2
     with pytest.raises(ValueError, match="attention_backend"):
         QuantizedDoubleStreamBlock(E, H, FFN, DEV, gen(710), attention_backend="flash4")
+
+
+@pytest.mark.parametrize("E,H,write_only", [(512, 4, False), (1024, 8, False), (1024, 8, True)])
+def test_block_fused_qkv_matches_unfused(E, H, write_only):
+    """The video stream's QKV projection with its q/k norm, RoPE and ring write in the GEMM
+    (fuse_qkv=True, the default) and as the GEMM followed by fused_qkv_norm_rope_cache: the same
+    block outputs and ring contents bit for bit (also the cache-only forward)."""
+    from joyomni_ops.dit_block import CachedChunk, KVRing, QuantizedDoubleStreamBlock
+    announce("block fused qkv vs unfused", E, H, write_only)
+    FFN, T, hh, ww = 3 * E, 32, 12, 20
+    L, D = hh * ww, E // H
+    img = torch.randn(1, L, E, generator=gen(727)).to(torch.bfloat16).to(DEV)
+    txt = torch.randn(1, T, E, generator=gen(728)).to(torch.bfloat16).to(DEV)
+    vec = torch.randn(1, E, generator=gen(729)).to(torch.bfloat16).to(DEV)
+    cos_h, sin_h = (t.to(DEV) for t in _half_tables([3], hh, ww))
+    cf, sf = (t.to(DEV) for t in _full_tables([0], hh, ww))
+    outs, rings = [], []
+    for fuse in (True, False):
+        blk = QuantizedDoubleStreamBlock(E, H, FFN, DEV, gen(730), fuse_qkv=fuse)
+        ring = KVRing(2, L, H, D, DEV)
+        ring.k[1].copy_(torch.randn(L, H, D, generator=gen(731)).to(torch.bfloat16))
+        ring.v[1].copy_(torch.randn(L, H, D, generator=gen(732)).to(torch.bfloat16))
+        ring.lengths[1] = L
+        outs.append(blk.forward(img, txt, vec, cos_h, sin_h, ring=ring, write_slot=0,
+                                cached=[CachedChunk(1, cf, sf)], kv_cache_write_only=write_only))
+        rings.append(ring)
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    assert torch.equal(rings[0].k.view(torch.int16), rings[1].k.view(torch.int16))
+    assert torch.equal(rings[0].v.view(torch.int16), rings[1].v.view(torch.int16))

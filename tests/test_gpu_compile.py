@@ -148,6 +148,12 @@ def _cases():
     cases.append((ops.fused_qkv_norm_rope_cache, (qkv, H, EPS, qw, kw, cos_h, sin_h, _bf(L, H, D, g=g),
                                                   _bf(L, H, D, g=g), _bf(2, L, H, D, g=g), _bf(2, L, H, D, g=g), 1, 0,
                                                   _bf(L, H, D, g=g), -1, True)))
+    aq, saq = _fp8(_bf(L, E, g=g))
+    wq, swq = _fp8(_bf(3 * E, E, g=g, scale=0.02))
+    cases.append((ops.fp8_qkv_norm_rope_cache, (aq, wq.t(), saq, swq.reshape(1, 3 * E), _bf(3 * E, g=g, scale=0.01),
+                                                H, EPS, qw, kw, cos_h, sin_h, _bf(L, H, D, g=g), _bf(L, H, D, g=g),
+                                                _bf(2, L, H, D, g=g), _bf(2, L, H, D, g=g), 1, 0, _bf(L, H, D, g=g),
+                                                -1, True)))
     img = qkv.view(1, L, 3, H, D)
     txt = _bf(1, T, 3, H, D, g=g)
     ck, cv = _bf(1, C, H, D, g=g), _bf(1, C, H, D, g=g)
@@ -205,11 +211,11 @@ def test_opcheck_covers_every_op():
     assert sorted(op._qualified_op_name.split("::")[1] for op, _ in _cases()) == _op_names()
 
 
-@pytest.mark.parametrize("index", range(17))
+@pytest.mark.parametrize("index", range(18))
 def test_opcheck(index):
     import joyomni_ops  # noqa: F401
     cases = _cases()
-    assert len(cases) == 17
+    assert len(cases) == 18
     op, args = cases[index]
     announce("opcheck", op._qualified_op_name)
     utils = ("test_schema", "test_autograd_registration", "test_faketensor", "test_aot_dispatch_dynamic")
