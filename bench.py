@@ -219,6 +219,56 @@ def bench_qkv(steps, warmup):
     return t, qkv_bytes(L_TOK)
 
 
+def bench_qkv_projection(steps, warmup):
+    """The video stream's QKV projection at the block's size (10800 tokens, K 5120, N 3 x 40 x 128)
+    with its q/k RMSNorm, RoPE and KV-ring write, as one op (fp8_qkv_norm_rope_cache: the norm, the
+    rotation and the ring write in the GEMM's epilogue) and as the two-op sequence it replaces
+    (fp8_scaled_mm into a bf16 [M, 3E] buffer, then fused_qkv_norm_rope_cache on it; dit.py:409-451),
+    with the GEMM alone beside them. Q, K and V go into views of joint buffers behind 21600 cached rows
+    and the ring slot, as in the block."""
+    import torch
+    import joyomni_ops as jo
+    dev = torch.device("cuda:0")
+    M, K, N = L_TOK, E, 3 * E
+    g = torch.Generator().manual_seed(3)
+    x = outlier_acts(M, K, g).to(dev)
+    wf = (0.02 * torch.randn(N, K, generator=g)).to(torch.bfloat16).to(dev)
+    a, sa = jo_quant(x)
+    w, sw = jo_quant(wf)
+    b, swr = w.t(), sw.reshape(1, N)
+    bias = (0.01 * torch.randn(N, generator=g)).to(torch.bfloat16).to(dev)
+    qw = (1 + 0.1 * torch.randn(HEAD_DIM, generator=g)).to(torch.bfloat16).to(dev)
+    kw = (1 + 0.1 * torch.randn(HEAD_DIM, generator=g)).to(torch.bfloat16).to(dev)
+    from joyomni_ops.rope import rope_3d_half_tables
+    cos, sin = rope_3d_half_tables(3, 45, 80, (44, 42, 42), 10000.0, device=dev)
+    C = 2 * L_TOK
+    q = torch.empty(1, M + 512, HEADS, HEAD_DIM, dtype=torch.bfloat16, device=dev)
+    kk = torch.empty(1, C + M + 512, HEADS, HEAD_DIM, dtype=torch.bfloat16, device=dev)
+    vv = torch.empty_like(kk)
+    ck = torch.empty(RING_SLOTS, M, HEADS, HEAD_DIM, dtype=torch.bfloat16, device=dev)
+    cv = torch.empty_like(ck)
+    outs = (q[0, :M], kk[0, C:C + M], ck, cv, SLOT, 0)
+
+    def two_op():
+        y = jo.fp8_scaled_mm(a, b, sa, swr, torch.bfloat16, bias)
+        jo.fused_qkv_norm_rope_cache(y, HEADS, 1e-6, qw, kw, cos, sin, *outs, v_out=vv[0, C:C + M])
+
+    def fused():
+        jo.fp8_qkv_norm_rope_cache(a, b, sa, swr, bias, HEADS, 1e-6, qw, kw, cos, sin, *outs, v_out=vv[0, C:C + M])
+
+    def gemm_only():
+        jo.fp8_scaled_mm(a, b, sa, swr, torch.bfloat16, bias)
+
+    n = min(steps, 20)
+    res = {}
+    for name, fn in (("two_op", two_op), ("fused", fused), ("gemm_only", gemm_only)):
+        res[name + "_us"] = time_launches(fn, n, warmup) * 1e6
+    res["shape"] = f"M{M} K{K} N{N}"
+    res["fused_speedup_vs_two_op"] = res["two_op_us"] / res["fused_us"]
+    res["fused_tflops"] = 2.0 * M * N * K / (res["fused_us"] * 1e-6) / 1e12
+    return res
+
+
 def bench_gemm(steps, warmup):
     import torch
     import joyomni_ops as jo
@@ -814,6 +864,10 @@ def summary(rec):
         out["cfg3_M_N_us_bound_frac_hipblaslt_us"] = [
             [x["M"], x["N"], r(x["us"]), x["roofline_bound"], r(x["frac_roofline"], 3), r(x["reference_hipblaslt_us"])]
             for x in rec["gemm_cfg3_small_m"]]
+    if "qkv_projection" in rec:
+        qp = rec["qkv_projection"]
+        out["qkv_projection_us"] = {"fused": r(qp["fused_us"], 0), "two_op": r(qp["two_op_us"], 0),
+                                    "gemm_only": r(qp["gemm_only_us"], 0)}
     if "cfg0_linear" in rec:
         out["cfg0_linear_us"] = r(rec["cfg0_linear"]["us"])
     if "act_quant" in rec:
@@ -848,7 +902,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time plain launches (no HIP graph)")
     ap.add_argument("--only", default="all",
-                    choices=["all", "qkv", "gemm", "cfg0", "refgemm", "small", "quant", "pack", "norm", "attn", "block",
+                    choices=["all", "qkv", "qkvproj", "gemm", "cfg0", "refgemm", "small", "quant", "pack", "norm", "attn", "block",
                              "copy", "clock"])
     ap.add_argument("--tunableop", metavar="CSV", default=None,
                     help="tune the reference's torch._scaled_mm legs with PyTorch TunableOp first, with the "
@@ -898,6 +952,11 @@ def main():
         progress(f"cfg2 GEMMs {agg:.0f} TFLOP/s aggregate")
         if "value" not in rec:
             rec.update({"value": round(agg, 1), "unit": "TFLOP/s", "ms_per_step": sum(r["ms"] for r in res)})
+    if args.only in ("all", "qkvproj"):
+        rec["qkv_projection"] = bench_qkv_projection(args.steps, args.warmup)
+        qp = rec["qkv_projection"]
+        progress(f"QKV projection + norm/RoPE/ring: fused {qp['fused_us']:.0f} us, two ops {qp['two_op_us']:.0f} us "
+                 f"(GEMM alone {qp['gemm_only_us']:.0f} us)")
     if args.only in ("all", "cfg0"):
         rec["cfg0_linear"] = bench_cfg0(args.steps, args.warmup)
         progress(f"cfg0 linear {rec['cfg0_linear']['us']:.1f} us")
