@@ -1687,6 +1687,167 @@ hipError_t launch_deepk(const GemmArgs& g, int splits, float* ws, hipStream_t st
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Narrow tiles for small M with N % 80 == 0 (the model's 5120-wide outputs at 129-512 tokens):
+// BM x 80 tiles, BM = 64 or 128, so that one round of tiles fills the CUs without a K split
+// (M 256 x N 5120: 4 x 64 tiles of 64 x 80; M 512: 4 x 64 of 128 x 80). These GEMMs are bound by
+// the operand bytes each CU streams, (BM + BN) x K per tile, at 40-50 GB/s per CU when the
+// operands come partly from HBM (a load-only probe of the same access pattern takes 18.8 us at
+// M 512 x N 5120 with 128 x 80 tiles against 25.1 us with 128 x 128 tiles on 160 CUs, and
+// 14.7 us at M 256 with 64 x 80 tiles); of the tile shapes that fill one round, the squarest
+// moves the fewest bytes per CU.
+//
+// 4 waves in 4 x 1: wave w owns rows [w BM/4, +BM/4) and all 80 columns, as FM x 5 tiles of
+// v_mfma_scale_f32_16x16x128_f8f6f4 (operand lanes and accumulator layout as in fp8_gemm_4q:
+// lane l holds row l % 16 of a fragment, K bytes [32 (l / 16), +32) of a 128-byte k-step;
+// accumulator element e of lane l is output (row l % 16, column 4 (l / 16) + e)). K steps of
+// 256 bytes staged global -> VGPR -> LDS as in fp8_gemm_4k: U staging buffers (2; 3 measured no
+// faster) and two LDS slots; iteration t loads step t + U into the buffer that held step t, runs
+// step t's MFMAs and writes step t + 1 into the slot of step t - 1 (read by every wave before the
+// barrier).
+// Workgroup positions are XCD-ordered with the tile rows innermost, so the tiles that share
+// a W panel run on one XCD and read it through one L2.
+// ---------------------------------------------------------------------------
+template <bool kBf16, int kEpi, int BM, int U>
+__global__ __launch_bounds__(256, 1) void fp8_gemm_4n(
+    const uint8_t* __restrict__ A, const uint8_t* __restrict__ W, const float* __restrict__ sa,
+    const float* __restrict__ sb, const uint16_t* __restrict__ bias, uint16_t* __restrict__ C,
+    int M, int N, int K, int64_t ldc, int tiles_m, ResidualArgs res) {
+  static_assert(kEpi == kEpiPlain || kEpi == kEpiGelu || kEpi == kEpiResidual, "epilogues");
+  static_assert(U == 2 || U == 3, "staging buffers");
+  constexpr int UNR = U == 2 ? 2 : 6;  // lcm(U, 2 slots)
+  constexpr int BN = 80, KS = 256, NW = 4;
+  constexpr int WTM = BM / NW, FM = WTM / 16, FN = BN / 16;
+  constexpr int CPR = KS / 16, RPI = 256 / CPR;   // 16 chunks per row, 16 rows per workgroup-wide load
+  constexpr int ROWS = BM + BN, L = ROWS / RPI;   // loads per thread and step
+  constexpr int SLOT = ROWS * KS, A_BYTES = BM * KS;
+  static_assert(BM == 64 || BM == 128, "tile heights");
+  static_assert(ROWS % RPI == 0 && BM % RPI == 0, "whole loads, each of A rows or of W rows");
+  static_assert(2 * SLOT <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * SLOT];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int pos = xcd_position(blockIdx.x, gridDim.x);
+  const int m0 = (pos % tiles_m) * BM, n0 = (pos / tiles_m) * BN;
+  const int nk = K / KS;
+
+  // operand rows of this thread's loads: load i covers rows 16 i .. 16 i + 15 of the slot (A rows,
+  // then W rows); the thread fetches logical chunk c ^ swz(row) into physical chunk c = tid % 16
+  const uint8_t* src[L];
+  const int lc = tid % CPR;
+#pragma unroll
+  for (int i = 0; i < L; ++i) {
+    const int row = i * RPI + tid / CPR;
+    const int chunk = (lc ^ swz_rows<KS>(row)) * 16;
+    src[i] = row < BM ? A + (int64_t)min(m0 + row, M - 1) * K + chunk : W + (int64_t)(n0 + row - BM) * K + chunk;
+  }
+  v4i stg[U][L];
+  auto gload = [&](auto bc, int kt) {
+    constexpr int B = decltype(bc)::value;
+    const int64_t koff = (int64_t)min(kt, nk - 1) * KS;
+#pragma unroll
+    for (int i = 0; i < L; ++i) stg[B][i] = *(const v4i*)(src[i] + koff);
+  };
+  auto lwrite = [&](auto bc, auto sc) {
+    constexpr int B = decltype(bc)::value, SL = decltype(sc)::value;
+    uint8_t* base = lds + SL * SLOT + tid * 16;
+#pragma unroll
+    for (int i = 0; i < L; ++i) *(v4i*)(base + i * 4096) = stg[B][i];
+  };
+
+  const int frow = lane & 15, g = lane >> 4;
+  const int a_row0 = (wave * WTM + frow) * KS, w_row0 = A_BYTES + frow * KS;
+  v4f acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j) acc[i][j] = (v4f){};
+  // fragment of k-step S (128 bytes: logical chunks 8 S + 2 g, + 1) of the row at r (the
+  // swizzle of every fragment row is frow)
+  auto frag = [&](const uint8_t* r, int s) {
+    const v4i lo = *(const v4i*)(r + (((8 * s + 2 * g) ^ frow) << 4));
+    const v4i hi = *(const v4i*)(r + (((8 * s + 2 * g + 1) ^ frow) << 4));
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  };
+  auto iteration = [&](auto jc, int t) {
+    constexpr int J = decltype(jc)::value;  // t % UNR
+    constexpr int SL = J % 2;
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): own LDS writes and fragment reads done
+    block_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    // into the buffer of step t (written to LDS in the last iteration); left to the compiler's
+    // schedule among the MFMAs (issued as a block before them: M 512 x N 5120 25.3 -> 28.7 us)
+    gload(IC<J % U>{}, t + U);
+    const uint8_t* slot = lds + SL * SLOT;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      v8i fa[FM], fw[FN];
+#pragma unroll
+      for (int j = 0; j < FM; ++j) fa[j] = frag(slot + a_row0 + j * 16 * KS, s);
+#pragma unroll
+      for (int i = 0; i < FN; ++i) fw[i] = frag(slot + w_row0 + i * 16 * KS, s);
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j) acc[i][j] = mfma_16x16x128_fp8(fw[i], fa[j], acc[i][j]);
+    }
+    lwrite(IC<(J + 1) % U>{}, IC<SL ^ 1>{});  // step t + 1 into the slot of step t - 1
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  static_for<0, U>([&](auto bc) { gload(bc, decltype(bc)::value); });
+  lwrite(IC<0>{}, IC<0>{});
+  int t = 0;
+  for (; t + UNR <= nk; t += UNR) static_for<0, UNR>([&](auto jc) { iteration(jc, t + decltype(jc)::value); });
+  static_for<0, UNR - 1>([&](auto jc) {
+    if (t + decltype(jc)::value < nk) iteration(jc, t + decltype(jc)::value);
+  });
+
+  // epilogue: out = round(fma(acc * sb[n], sa[m], bias[n])), then GELU or the gated residual;
+  // each lane stores 4 consecutive outputs (8 bytes) of one row per MFMA tile
+#pragma unroll
+  for (int j = 0; j < FM; ++j) {
+    const int m = m0 + wave * WTM + j * 16 + frow;
+    if (m >= M) continue;
+    const float s_a = sa[m];
+#pragma unroll
+    for (int i = 0; i < FN; ++i) {
+      const int n = n0 + i * 16 + 4 * g;
+      const float4 sv = *(const float4*)(sb + n);
+      const uint2 bb = bias ? *(const uint2*)(bias + n) : make_uint2(0u, 0u);
+      const float sbe[4] = {sv.x, sv.y, sv.z, sv.w};
+      const float be[4] = {unpack_lo<kBf16>(bb.x), unpack_hi<kBf16>(bb.x), unpack_lo<kBf16>(bb.y),
+                           unpack_hi<kBf16>(bb.y)};
+      float o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = __builtin_fmaf(acc[i][j][e] * sbe[e], s_a, be[e]);
+      uint2 pk = make_uint2(pack2<kBf16>(o[0], o[1]), pack2<kBf16>(o[2], o[3]));
+      if constexpr (kEpi == kEpiGelu) {
+        pk = make_uint2(pack2<kBf16>(gelu_tanh(unpack_lo<kBf16>(pk.x)), gelu_tanh(unpack_hi<kBf16>(pk.x))),
+                        pack2<kBf16>(gelu_tanh(unpack_lo<kBf16>(pk.y)), gelu_tanh(unpack_hi<kBf16>(pk.y))));
+      }
+      if constexpr (kEpi == kEpiResidual) {
+        const uint2 x = *(const uint2*)(res.ptr + (int64_t)m * res.ld + n);
+        const uint2 gt = *(const uint2*)(res.gate + n);
+        pk = make_uint2(gated_pair<kBf16>(pk.x, x.x, gt.x), gated_pair<kBf16>(pk.y, x.y, gt.y));
+      }
+      *(uint2*)(C + (int64_t)m * ldc + n) = pk;
+    }
+  }
+}
+
+// One round of BM x 80 tiles (fp8_gemm_4n).
+template <bool kBf16, int kEpi, int BM, int U>
+hipError_t launch_narrow(const GemmArgs& g, hipStream_t st) {
+  const int tm = (g.M + BM - 1) / BM, tn = g.N / 80;
+  hipLaunchKernelGGL((fp8_gemm_4n<kBf16, kEpi, BM, U>), dim3(tm * tn), dim3(256), 0, st, (const uint8_t*)g.A,
+                     (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N,
+                     g.K, g.ldc, tm, residual_args(g));
+  return hipGetLastError();
+}
+
 // Small M (<= 512 rows): deep-K tiles (fp8_gemm_4k), split over K where the tiles
 // alone would leave most CUs idle (splits = CUs / tiles, at most 8 and at least 4 K
 // steps per split). Measured on MI355X with W read from HBM, K 5120 unless stated;
@@ -1736,8 +1897,27 @@ SmallPlan small_plan(int M, int N, int K, bool allow_split) {
   return SmallPlan{2, splits_for(tiles(128, 128), 128)};
 }
 
+// Tile height of the narrow-tile plan (fp8_gemm_4n), or 0: one round of BM x 80 tiles where it
+// fills the CUs (N 5120: 64-row tiles at 129-256 rows, 128-row tiles at 449-512 rows with K below
+// 8192). Measured against the deep-K plans (W from HBM, graph-replayed, K 5120): M 200 20.2 ->
+// 15.8 us, M 256 21.9 -> 17.3 (no K split, no reduce launch), M 512 29.0 -> 25.3 (256 tiles
+// against 160), with the gated residual 31.8 -> 26.7. Where the deep-K plan splits K over
+// larger tiles it moves fewer bytes per CU and stays ahead: M 300 (3 x 64 tiles of 128 x 80)
+// 24.8 vs 22.3 us, M 512 x K 13824 56.3 vs 50.7.
+int narrow_bm(int M, int N, int K) {
+  if (N % 80 != 0 || K % 256 != 0 || M <= 128 || M > kSmallMaxM) return 0;
+  const int P = device_cus(), tn = N / 80;
+  const int t128 = ((M + 127) / 128) * tn, t64 = ((M + 63) / 64) * tn;
+  if (8 * t128 >= 7 * P && t128 <= P && K < 8192) return 128;
+  if (4 * t64 >= 3 * P && t64 <= P) return 64;
+  return 0;
+}
+
 template <bool kBf16, int kEpi>
 hipError_t launch_small_m(const GemmArgs& g, hipStream_t st) {
+  const int nbm = narrow_bm(g.M, g.N, g.K);
+  if (nbm == 128) return launch_narrow<kBf16, kEpi, 128, 2>(g, st);
+  if (nbm == 64) return launch_narrow<kBf16, kEpi, 64, 2>(g, st);
   if (g.M > 256 && g.K % 128 == 0) {
     // 257-512 rows where 256x128 tiles fill 3/4 of the CUs: one tile per workgroup with
     // 128-byte K steps through the DMA ring (M 512 x N 15360: 43-45 us vs 47 for 128x256
@@ -1897,7 +2077,7 @@ __global__ __launch_bounds__(256) void qkv_tail_norm_rope(const uint16_t* __rest
 }  // namespace
 
 int64_t fp8_gemm_workspace_bytes(int M, int N, int K) {
-  if (K < 64 || K % 64 != 0 || N % 8 != 0) return 0;
+  if (K < 64 || K % 64 != 0 || N % 8 != 0 || narrow_bm(M, N, K) != 0) return 0;
   const SmallPlan p = small_plan(M, N, K, true);
   return p.splits > 1 ? (int64_t)p.splits * M * N * 4 : 0;
 }

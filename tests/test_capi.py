@@ -81,14 +81,19 @@ def test_gemm_argument_checks(lib):
 
 
 def test_gemm_workspace_size(lib):
-    """Host-side plan: split-K only for small M where the tiles leave CUs idle (256-CU MI355X
-    when no device is visible); the size is splits * M * N fp32 partial sums."""
+    """Host-side plan: split-K only for small M where the tiles leave CUs idle and no narrow-tile
+    plan fills them (256-CU MI355X when no device is visible); the size is splits * M * N fp32
+    partial sums."""
     size = lib.joy_fp8_scaled_mm_workspace_size
     ws = size(64, 5120, 5120)
     assert ws > 0 and ws % (64 * 5120 * 4) == 0 and 2 <= ws // (64 * 5120 * 4) <= 8
     assert size(10800, 5120, 5120) == 0      # large M: full rounds of 256x256 tiles, no split
     assert size(64, 15360, 5120) == 0        # 240 tiles already cover the CUs
     assert size(64, 5120, 5120 + 64) == 0    # K not a multiple of the plan's K step
+    # N % 80 == 0 where one round of 80-column tiles fills the CUs: no split
+    assert size(256, 5120, 5120) == 0 and size(200, 5120, 768) == 0 and size(512, 5120, 5120) == 0
+    assert size(256, 5136, 5120) > 0         # the same rows with 128x128 tiles split over K
+    assert size(512, 5120, 13824) > 0        # long K: larger tiles split over K move fewer bytes
     assert size(0, 5120, 5120) == 0 and size(-1, 8, 64) == 0 and size(64, 36, 64) == 0
 
 

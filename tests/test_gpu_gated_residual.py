@@ -90,7 +90,10 @@ def test_exact_fp16():
                                    (2048, 5120, 13824), (777, 1000, 320),
                                    # persistent 256x256 kernel (K % 256 == 0, M % 4 == 0): a whole
                                    # round plus a sub-tile tail, and a single partial round
-                                   (4352, 4352, 512), (2600, 2304, 512)])
+                                   (4352, 4352, 512), (2600, 2304, 512),
+                                   # narrow 80-column tiles (the condition stream's 512-token
+                                   # projections; 64-row tiles with padding rows)
+                                   (512, 5120, 5120), (200, 5120, 768)])
 def test_random_equals_addcmul_over_plain_gemm(dtype, M, N, K):
     """Large / every-launch-shape problems: the fused epilogue equals torch.addcmul applied to
     fp8_scaled_mm's own output (the same kernel tiling sums each output in the same order)."""

@@ -279,7 +279,12 @@ def gemm_capi(qa_u8, qw_u8, sa, sw, bias_u16, out_dtype, workspace):
 SMALL_M_PLAN_SHAPES = [(64, 5120, 5120), (33, 1032, 4096), (1, 264, 2048), (64, 15360, 256),
                        (200, 2056, 2048), (256, 5120, 1280), (129, 4104, 3072), (300, 2056, 1664),
                        (512, 5120, 13824), (400, 12296, 1152), (320, 15360, 512), (512, 5120, 5120),
-                       (48, 1544, 2560)]
+                       (48, 1544, 2560),
+                       # narrow 80-column tiles (one round, no split): 128-row tiles with a partial
+                       # last tile row, 64-row tiles with padding rows, one K step, an odd step count;
+                       # beside them shapes that keep the deep-K plans (300 rows, N 5136)
+                       (448, 5120, 512), (200, 5120, 768), (129, 5120, 256), (256, 5120, 2816),
+                       (300, 5120, 1024), (512, 5136, 13824)]
 
 
 @pytest.mark.parametrize("M,N,K", SMALL_M_PLAN_SHAPES)
@@ -302,7 +307,7 @@ def test_small_m_plans_exact_with_and_without_workspace(M, N, K):
     assert np.array_equal(u16(y_nows), exp_bits)
 
 
-@pytest.mark.parametrize("M,N,K", [(64, 5120, 5120), (256, 5120, 5120), (512, 5120, 13824), (300, 2056, 1664)])
+@pytest.mark.parametrize("M,N,K", [(64, 5120, 5120), (256, 5136, 5120), (512, 5136, 13824), (300, 2056, 1664)])
 def test_split_k_workspace_needs_no_initialisation(M, N, K):
     """The split-K workspace needs no initialisation: whatever it holds before a call -- random bytes,
     all ones, what the previous call of this or another shape left, zeros -- every split writes its
@@ -319,7 +324,7 @@ def test_split_k_workspace_needs_no_initialisation(M, N, K):
     exp_bits, _ = og.scaled_mm(qa, qw, sa, sw, bias)
     need = jo._LIB.joy_fp8_scaled_mm_workspace_size(M, N, K)
     assert need > 0, "shape expected to use a K split"
-    other = (64, 5120, 5120) if (M, N, K) != (64, 5120, 5120) else (256, 5120, 5120)
+    other = (64, 5120, 5120) if (M, N, K) != (64, 5120, 5120) else (256, 5136, 5120)
     need_other = jo._LIB.joy_fp8_scaled_mm_workspace_size(*other)
     ws = torch.empty(max(need, need_other), dtype=torch.uint8, device=DEV)
     fills = [("random bytes", lambda: ws.copy_(torch.randint(0, 256, ws.shape, dtype=torch.uint8, device=DEV))),
@@ -340,7 +345,7 @@ def test_split_k_workspace_needs_no_initialisation(M, N, K):
         assert np.array_equal(u16(y), exp_bits), name
 
 
-@pytest.mark.parametrize("M,N,K", [(64, 5120, 5120), (256, 5120, 5120), (512, 5120, 13824)])
+@pytest.mark.parametrize("M,N,K", [(64, 5120, 5120), (256, 5136, 5120), (512, 5136, 13824)])
 def test_small_m_split_random_within_tolerance(M, N, K):
     """cfg-0 distributions through a split plan: the benchmark's tolerance and the accumulation bound,
     and the split and unsplit launches agree to the same bound."""
@@ -356,7 +361,8 @@ def test_small_m_split_random_within_tolerance(M, N, K):
 
 
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("M,N,K", [(200, 520, 512), (64, 2048, 4096), (300, 2560, 5120), (400, 12296, 512)])
+@pytest.mark.parametrize("M,N,K", [(200, 520, 512), (64, 2048, 4096), (300, 2560, 5120), (400, 12296, 512),
+                                   (512, 5120, 512), (200, 5120, 768)])
 def test_gelu_epilogue_and_fp16_out_plans(out_dtype, M, N, K):
     """GELU-tanh on the rounded output, on unsplit and split small-M plans and the one-tile 256x128
     plan of 257-512 rows (400 x 12296: 194 tiles, a partial last tile column)."""
