@@ -1697,67 +1697,75 @@ hipError_t launch_deepk(const GemmArgs& g, int splits, float* ws, hipStream_t st
 // 14.7 us at M 256 with 64 x 80 tiles); of the tile shapes that fill one round, the squarest
 // moves the fewest bytes per CU.
 //
-// 4 waves in 4 x 1: wave w owns rows [w BM/4, +BM/4) and all 80 columns, as FM x 5 tiles of
+// 4 x KH waves: wave w owns rows [(w % 4) BM/4, +BM/4) and all 80 columns, as FM x 5 tiles of
 // v_mfma_scale_f32_16x16x128_f8f6f4 (operand lanes and accumulator layout as in fp8_gemm_4q:
 // lane l holds row l % 16 of a fragment, K bytes [32 (l / 16), +32) of a 128-byte k-step;
 // accumulator element e of lane l is output (row l % 16, column 4 (l / 16) + e)). K steps of
 // 256 bytes staged global -> VGPR -> LDS as in fp8_gemm_4k: U staging buffers (2; 3 measured no
 // faster) and two LDS slots; iteration t loads step t + U into the buffer that held step t, runs
 // step t's MFMAs and writes step t + 1 into the slot of step t - 1 (read by every wave before the
-// barrier).
+// barrier). With KH = 2 the waves w and w + 4 share a row group, each taking one of the two MFMA
+// k-steps of every K step (two waves per SIMD, so one wave's MFMAs run while the other waits);
+// their sums are added at the end, (k-step 0) + (k-step 1), through LDS.
 // Workgroup positions are XCD-ordered with the tile rows innermost, so the tiles that share
 // a W panel run on one XCD and read it through one L2.
 // ---------------------------------------------------------------------------
-template <bool kBf16, int kEpi, int BM, int U>
-__global__ __launch_bounds__(256, 1) void fp8_gemm_4n(
+template <bool kBf16, int kEpi, int BM, int U, int KH>
+__global__ __launch_bounds__(256 * KH, 1) void fp8_gemm_4n(
     const uint8_t* __restrict__ A, const uint8_t* __restrict__ W, const float* __restrict__ sa,
     const float* __restrict__ sb, const uint16_t* __restrict__ bias, uint16_t* __restrict__ C,
     int M, int N, int K, int64_t ldc, int tiles_m, ResidualArgs res) {
   static_assert(kEpi == kEpiPlain || kEpi == kEpiGelu || kEpi == kEpiResidual, "epilogues");
   static_assert(U == 2 || U == 3, "staging buffers");
+  static_assert(KH == 1 || KH == 2, "waves per row group");
   constexpr int UNR = U == 2 ? 2 : 6;  // lcm(U, 2 slots)
-  constexpr int BN = 80, KS = 256, NW = 4;
+  constexpr int BN = 80, KS = 256, NW = 4, NT = 256 * KH;
   constexpr int WTM = BM / NW, FM = WTM / 16, FN = BN / 16;
-  constexpr int CPR = KS / 16, RPI = 256 / CPR;   // 16 chunks per row, 16 rows per workgroup-wide load
-  constexpr int ROWS = BM + BN, L = ROWS / RPI;   // loads per thread and step
-  constexpr int SLOT = ROWS * KS, A_BYTES = BM * KS;
+  constexpr int CPR = KS / 16;                                 // 16 chunks per row
+  constexpr int ROWS = BM + BN, CHUNKS = ROWS * CPR;
+  constexpr int L = (CHUNKS + NT - 1) / NT, LAST = CHUNKS - (L - 1) * NT;  // loads per thread; the last
+  constexpr int SLOT = ROWS * KS, A_BYTES = BM * KS;                         // one by the first LAST threads
   static_assert(BM == 64 || BM == 128, "tile heights");
-  static_assert(ROWS % RPI == 0 && BM % RPI == 0, "whole loads, each of A rows or of W rows");
+  static_assert(LAST % 64 == 0 && (NT / CPR) % 16 == 0 && BM % (NT / CPR) == 0, "whole waves per load, A or W rows");
   static_assert(2 * SLOT <= 160 * 1024, "LDS");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * SLOT];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rg = wave % NW, kh = wave / NW;  // row group; the MFMA k-step (of 2 per K step) with KH = 2
   const int pos = xcd_position(blockIdx.x, gridDim.x);
   const int m0 = (pos % tiles_m) * BM, n0 = (pos / tiles_m) * BN;
   const int nk = K / KS;
 
-  // operand rows of this thread's loads: load i covers rows 16 i .. 16 i + 15 of the slot (A rows,
-  // then W rows); the thread fetches logical chunk c ^ swz(row) into physical chunk c = tid % 16
+  // operand rows of this thread's loads: load i covers rows NT/16 i .. of the slot (A rows, then W
+  // rows); the thread fetches logical chunk c ^ swz(row) into physical chunk c = tid % 16
   const uint8_t* src[L];
   const int lc = tid % CPR;
 #pragma unroll
   for (int i = 0; i < L; ++i) {
-    const int row = i * RPI + tid / CPR;
+    const int row = min(i * (NT / CPR) + tid / CPR, ROWS - 1);
     const int chunk = (lc ^ swz_rows<KS>(row)) * 16;
     src[i] = row < BM ? A + (int64_t)min(m0 + row, M - 1) * K + chunk : W + (int64_t)(n0 + row - BM) * K + chunk;
   }
+  const bool last = LAST == NT || tid < LAST;  // wave-uniform
   v4i stg[U][L];
   auto gload = [&](auto bc, int kt) {
     constexpr int B = decltype(bc)::value;
     const int64_t koff = (int64_t)min(kt, nk - 1) * KS;
 #pragma unroll
-    for (int i = 0; i < L; ++i) stg[B][i] = *(const v4i*)(src[i] + koff);
+    for (int i = 0; i < L; ++i)
+      if (i + 1 < L || last) stg[B][i] = *(const v4i*)(src[i] + koff);
   };
   auto lwrite = [&](auto bc, auto sc) {
     constexpr int B = decltype(bc)::value, SL = decltype(sc)::value;
     uint8_t* base = lds + SL * SLOT + tid * 16;
 #pragma unroll
-    for (int i = 0; i < L; ++i) *(v4i*)(base + i * 4096) = stg[B][i];
+    for (int i = 0; i < L; ++i)
+      if (i + 1 < L || last) *(v4i*)(base + i * NT * 16) = stg[B][i];
   };
 
   const int frow = lane & 15, g = lane >> 4;
-  const int a_row0 = (wave * WTM + frow) * KS, w_row0 = A_BYTES + frow * KS;
+  const int a_row0 = (rg * WTM + frow) * KS, w_row0 = A_BYTES + frow * KS;
   v4f acc[FN][FM];
 #pragma unroll
   for (int i = 0; i < FN; ++i)
@@ -1782,12 +1790,13 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4n(
     gload(IC<J % U>{}, t + U);
     const uint8_t* slot = lds + SL * SLOT;
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
+    for (int s = 0; s < 2 / KH; ++s) {
+      const int ks = KH == 2 ? kh : s;
       v8i fa[FM], fw[FN];
 #pragma unroll
-      for (int j = 0; j < FM; ++j) fa[j] = frag(slot + a_row0 + j * 16 * KS, s);
+      for (int j = 0; j < FM; ++j) fa[j] = frag(slot + a_row0 + j * 16 * KS, ks);
 #pragma unroll
-      for (int i = 0; i < FN; ++i) fw[i] = frag(slot + w_row0 + i * 16 * KS, s);
+      for (int i = 0; i < FN; ++i) fw[i] = frag(slot + w_row0 + i * 16 * KS, ks);
 #pragma unroll
       for (int i = 0; i < FN; ++i)
 #pragma unroll
@@ -1804,12 +1813,31 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4n(
   static_for<0, UNR - 1>([&](auto jc) {
     if (t + decltype(jc)::value < nk) iteration(jc, t + decltype(jc)::value);
   });
+  if constexpr (KH == 2) {
+    // the second k-step's sums join the first's: acc = acc(k-step 0) + acc(k-step 1)
+    wait_vmcnt_lgkm0<0>();  // also the last, unused prefetches
+    block_barrier();
+    v4f* xch = (v4f*)lds + (rg * FN * FM) * 64 + lane;
+    if (kh == 1) {
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j) xch[(i * FM + j) * 64] = acc[i][j];
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    block_barrier();
+    if (kh == 1) return;
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j) acc[i][j] += xch[(i * FM + j) * 64];
+  }
 
   // epilogue: out = round(fma(acc * sb[n], sa[m], bias[n])), then GELU or the gated residual;
   // each lane stores 4 consecutive outputs (8 bytes) of one row per MFMA tile
 #pragma unroll
   for (int j = 0; j < FM; ++j) {
-    const int m = m0 + wave * WTM + j * 16 + frow;
+    const int m = m0 + rg * WTM + j * 16 + frow;
     if (m >= M) continue;
     const float s_a = sa[m];
 #pragma unroll
@@ -1839,10 +1867,10 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4n(
 }
 
 // One round of BM x 80 tiles (fp8_gemm_4n).
-template <bool kBf16, int kEpi, int BM, int U>
+template <bool kBf16, int kEpi, int BM, int U, int KH>
 hipError_t launch_narrow(const GemmArgs& g, hipStream_t st) {
   const int tm = (g.M + BM - 1) / BM, tn = g.N / 80;
-  hipLaunchKernelGGL((fp8_gemm_4n<kBf16, kEpi, BM, U>), dim3(tm * tn), dim3(256), 0, st, (const uint8_t*)g.A,
+  hipLaunchKernelGGL((fp8_gemm_4n<kBf16, kEpi, BM, U, KH>), dim3(tm * tn), dim3(256 * KH), 0, st, (const uint8_t*)g.A,
                      (const uint8_t*)g.W, g.scales_a, g.scales_b, (const uint16_t*)g.bias, (uint16_t*)g.C, g.M, g.N,
                      g.K, g.ldc, tm, residual_args(g));
   return hipGetLastError();
@@ -1900,8 +1928,8 @@ SmallPlan small_plan(int M, int N, int K, bool allow_split) {
 // Tile height of the narrow-tile plan (fp8_gemm_4n), or 0: one round of BM x 80 tiles where it
 // fills the CUs (N 5120: 64-row tiles at 129-256 rows, 128-row tiles at 449-512 rows with K below
 // 8192). Measured against the deep-K plans (W from HBM, graph-replayed, K 5120): M 200 20.2 ->
-// 15.8 us, M 256 21.9 -> 17.3 (no K split, no reduce launch), M 512 29.0 -> 25.3 (256 tiles
-// against 160), with the gated residual 31.8 -> 26.7. Where the deep-K plan splits K over
+// 15.8 us, M 256 21.9 -> 17.3 (no K split, no reduce launch), M 512 29.0 -> 24.6 (256 tiles
+// against 160), with the gated residual 31.8 -> 25.4. Where the deep-K plan splits K over
 // larger tiles it moves fewer bytes per CU and stays ahead: M 300 (3 x 64 tiles of 128 x 80)
 // 24.8 vs 22.3 us, M 512 x K 13824 56.3 vs 50.7.
 int narrow_bm(int M, int N, int K) {
@@ -1916,8 +1944,10 @@ int narrow_bm(int M, int N, int K) {
 template <bool kBf16, int kEpi>
 hipError_t launch_small_m(const GemmArgs& g, hipStream_t st) {
   const int nbm = narrow_bm(g.M, g.N, g.K);
-  if (nbm == 128) return launch_narrow<kBf16, kEpi, 128, 2>(g, st);
-  if (nbm == 64) return launch_narrow<kBf16, kEpi, 64, 2>(g, st);
+  // 128-row tiles with two waves per row group (each one of the two MFMA k-steps of a K step): 25.3 ->
+  // 24.6 us at M 512 x N 5120; 64-row tiles with one (two: 17.4 -> 18.3 us at M 256)
+  if (nbm == 128) return launch_narrow<kBf16, kEpi, 128, 2, 2>(g, st);
+  if (nbm == 64) return launch_narrow<kBf16, kEpi, 64, 2, 1>(g, st);
   if (g.M > 256 && g.K % 128 == 0) {
     // 257-512 rows where 256x128 tiles fill 3/4 of the CUs: one tile per workgroup with
     // 128-byte K steps through the DMA ring (M 512 x N 15360: 43-45 us vs 47 for 128x256
