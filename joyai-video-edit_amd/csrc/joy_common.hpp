@@ -96,6 +96,13 @@ __device__ __forceinline__ uint32_t pack_fp8x4(float a, float b, float c, float 
   return w;
 }
 
+// The same bytes as pack_fp8x4 without a zeroed register: the first conversion keeps the upper
+// half of its destination, which the second overwrites, so a's bits may stand there.
+__device__ __forceinline__ uint32_t pack_fp8x4_reuse(float a, float b, float c, float d) {
+  const uint32_t w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, (int)__float_as_uint(a), false);
+  return __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+}
+
 // Clamp to the finite e4m3fn range; NaN passes through like torch.clamp.
 __device__ __forceinline__ float clamp_fp8(float v) {
   v = v > kFp8Max ? kFp8Max : v;

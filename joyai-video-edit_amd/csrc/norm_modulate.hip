@@ -515,29 +515,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void n
     }
     if constexpr (kFp8) {
       amax = (amax & 0xffffu) > (amax >> 16) ? (amax & 0xffffu) : (amax >> 16);
-      amax = wave_max_u32(amax);
+      // wave-uniform, so that the quantisation below takes one scalar branch per row rather than
+      // an exec-mask branch per vector
+      amax = __builtin_amdgcn_readfirstlane(wave_max_u32(amax));
       float s;
       const bool finite = fp8_row_scale<kFp16>(amax, s);
       if (lane == 0) a.out_s[row] = s;
       const float rs = 1.0f / s;
       uint2* dst = (uint2*)((uint8_t*)a.out_q + row * N);
+      if (finite) {  // no clamp needed (see norm_mod_rows)
 #pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        uint2 o;
-        if (finite) {  // no clamp needed (see norm_mod_rows)
+        for (int i = 0; i < NV; ++i) {
           float q[8];
 #pragma unroll
           for (int j = 0; j < 8; ++j) q[j] = kDivide ? div_by_scale(f[i][j], s, rs) : f[i][j] * rs;
-          o.x = pack_fp8x4(q[0], q[1], q[2], q[3]);
-          o.y = pack_fp8x4(q[4], q[5], q[6], q[7]);
-        } else {
+          nt_store8(dst + lane + 64 * i, make_uint2(pack_fp8x4_reuse(q[0], q[1], q[2], q[3]),
+                                                    pack_fp8x4_reuse(q[4], q[5], q[6], q[7])));
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
           uint32_t bq[8];
 #pragma unroll
           for (int j = 0; j < 8; ++j) bq[j] = e4m3fn_soft(clamp_fp8(kDivide ? f[i][j] / s : f[i][j] * rs));
-          o.x = bq[0] | (bq[1] << 8) | (bq[2] << 16) | (bq[3] << 24);
-          o.y = bq[4] | (bq[5] << 8) | (bq[6] << 16) | (bq[7] << 24);
+          nt_store8(dst + lane + 64 * i, make_uint2(bq[0] | (bq[1] << 8) | (bq[2] << 16) | (bq[3] << 24),
+                                                    bq[4] | (bq[5] << 8) | (bq[6] << 16) | (bq[7] << 24)));
         }
-        nt_store8(dst + lane + 64 * i, o);
       }
     }
   }
