@@ -217,7 +217,10 @@ JOY_API joy_status joy_fused_qkv_norm_rope_cache(const void *qkv, int64_t qkv_ro
  * GEMM arguments as joy_fp8_scaled_mm (mat_b: [3*num_heads*head_dim, K] e4m3fn, bias bf16 or
  * NULL); norm/RoPE/ring arguments as joy_fused_qkv_norm_rope_cache (cos/sin [M, head_dim/2]).
  * scratch: 16-byte aligned device memory of at least joy_fp8_qkv_norm_rope_cache_scratch_size
- * bytes (may be NULL when that is 0).
+ * bytes (may be NULL when that is 0) when cos / sin are 16-byte aligned and every output's
+ * ((rows - 1) * stride + num_heads * head_dim) * 2 is below 2^31; otherwise M * 3 * num_heads *
+ * head_dim * 2 bytes (the call then runs the GEMM and the standalone kernel). Too little
+ * scratch for the call is JOY_ERR_INVALID_ARGUMENT, before any launch.
  */
 JOY_API joy_status joy_fp8_qkv_norm_rope_cache(const void *mat_a, const void *mat_b, const float *scales_a,
                                                const float *scales_b, const void *bias, int64_t M, int64_t K,
@@ -230,7 +233,8 @@ JOY_API joy_status joy_fp8_qkv_norm_rope_cache(const void *mat_a, const void *ma
                                                int64_t cache_tokens, int cache_post_rope, void *scratch,
                                                int64_t scratch_bytes, void *stream);
 
-/* Bytes of scratch joy_fp8_qkv_norm_rope_cache needs (0 when every tile takes the fused epilogue). */
+/* Bytes of scratch joy_fp8_qkv_norm_rope_cache needs with 16-byte aligned cos / sin and outputs of
+ * token stride num_heads * head_dim (0 when every tile takes the fused epilogue). */
 JOY_API int64_t joy_fp8_qkv_norm_rope_cache_scratch_size(int64_t M, int64_t K, int64_t num_heads,
                                                          int64_t head_dim);
 

@@ -406,15 +406,19 @@ joy_status joy_fp8_qkv_norm_rope_cache(const void* mat_a, const void* mat_b, con
   const int64_t N = 3 * num_heads * head_dim;
   if (scratch_bytes < 0 || (scratch_bytes > 0 && !scratch))
     return fail(JOY_ERR_INVALID_ARGUMENT, "scratch_bytes must be >= 0, with a scratch buffer when > 0");
-  const int64_t need = joy_fp8_qkv_norm_rope_cache_scratch_size(M, K, num_heads, head_dim);
-  if (scratch_bytes < need)
-    return fail(JOY_ERR_INVALID_ARGUMENT, "fp8_qkv_norm_rope_cache: %lld bytes of scratch needed, %lld given",
-                (long long)need, (long long)scratch_bytes);
   joy::GemmArgs g;
   bool empty_g;
   st = gemm_args(mat_a, mat_b, scales_a, scales_b, bias, scratch, JOY_DTYPE_BF16, M, N, K, JOY_EPILOGUE_NONE, nullptr,
                  0, nullptr, nullptr, 0, true, g, &empty_g);
   if (st != JOY_OK || empty_n || empty_g) return st;
+  // the size query's figure, or M x N bf16 where this call's pointers or strides rule the fused
+  // epilogue out (cos / sin not 16-byte aligned, output offsets past 2^31 bytes)
+  const int64_t need = joy::fp8_gemm_qkv_call_scratch_bytes(g, a, (int)head_dim);
+  if (scratch_bytes < need)
+    return fail(JOY_ERR_INVALID_ARGUMENT,
+                "fp8_qkv_norm_rope_cache: %lld bytes of scratch needed for this call, %lld given (cos/sin not "
+                "16-byte aligned or output offsets past 2^31 bytes need the M x 3*num_heads*head_dim bf16 buffer)",
+                (long long)need, (long long)scratch_bytes);
   return hip_status(joy::launch_fp8_gemm_qkv(g, a, (int)head_dim, (hipStream_t)stream),
                     "fp8_qkv_norm_rope_cache launch");
 }

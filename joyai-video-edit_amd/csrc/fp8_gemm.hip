@@ -2165,6 +2165,12 @@ int64_t fp8_gemm_qkv_scratch_bytes(int M, int N, int K, int num_heads, int head_
   return (int64_t)M * N * 2;
 }
 
+int64_t fp8_gemm_qkv_call_scratch_bytes(const GemmArgs& g, const NormRopeArgs& a, int head_dim) {
+  if (g.M <= 0 || g.N <= 0) return 0;
+  if (qkv_fusable(g, a, head_dim) && qkv_plan(g.M, g.N).rem == 0) return 0;
+  return (int64_t)g.M * g.N * 2;
+}
+
 hipError_t launch_fp8_gemm_qkv(const GemmArgs& g, const NormRopeArgs& a, int head_dim, hipStream_t st) {
   if (g.M == 0 || g.N == 0) return hipSuccess;
   if (!qkv_fusable(g, a, head_dim) || (qkv_plan(g.M, g.N).rem > 0 && g.C == nullptr)) {

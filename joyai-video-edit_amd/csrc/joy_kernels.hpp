@@ -125,6 +125,9 @@ hipError_t launch_fp8_gemm(const GemmArgs& g, hipStream_t st);
 // scratch for the tiles (or the whole GEMM) that go through the standalone kernel.
 hipError_t launch_fp8_gemm_qkv(const GemmArgs& g, const NormRopeArgs& a, int head_dim, hipStream_t st);
 int64_t fp8_gemm_qkv_scratch_bytes(int M, int N, int K, int num_heads, int head_dim);
+// The scratch a given call needs: also counts what only the call's pointers and strides decide
+// (16-byte aligned cos / sin, 31-bit output offsets), which send it to the unfused path.
+int64_t fp8_gemm_qkv_call_scratch_bytes(const GemmArgs& g, const NormRopeArgs& a, int head_dim);
 // Workspace bytes the GEMM of this shape can use on the current device (0: none).
 int64_t fp8_gemm_workspace_bytes(int M, int N, int K);
 hipError_t launch_norm_modulate(const NormModArgs& a, hipStream_t st);

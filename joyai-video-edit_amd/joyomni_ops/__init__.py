@@ -401,8 +401,15 @@ def _fp8_qkv_norm_rope_cache_cuda(mat_a, mat_b, scales_a, scales_b, bias, num_he
     D = N // (3 * H)
     strides, n_slots, cap, n_cache = _norm_rope_out_checks(M, H, D, mat_a.device, q_weight, k_weight, cos, sin,
                                                            q_out, k_out, cache_k, cache_v, v_out, cache_tokens)
+    # the fused epilogue reads the tables 16 bytes at a time: an aligned copy of a misaligned view
+    cos = cos if cos.data_ptr() % 16 == 0 else cos.clone()
+    sin = sin if sin.data_ptr() % 16 == 0 else sin.clone()
     with torch.cuda.device(mat_a.device):
         nbytes = _LIB.joy_fp8_qkv_norm_rope_cache_scratch_size(M, K, H, D)
+        # outputs whose byte offsets pass 2^31 take the unfused path, through an [M, N] bf16 buffer
+        if any(t is not None and (M * st_ + H * D) * 2 > 0x7FFFFFFF
+               for t, st_ in ((q_out, strides[0]), (k_out, strides[1]), (v_out, strides[2]))):
+            nbytes = M * N * 2
         # the tiles that do not take the fused epilogue pass through this [M, N] bf16 buffer
         scratch = torch.empty(nbytes, dtype=torch.uint8, device=mat_a.device) if nbytes > 0 else None
         st = _LIB.joy_fp8_qkv_norm_rope_cache(

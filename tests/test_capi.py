@@ -140,6 +140,26 @@ def test_norm_rope_argument_checks(lib):
              0, 0, 0, 0, None) == 0
 
 
+def test_fused_qkv_projection_scratch_checks(lib):
+    """The QKV projection with norm/RoPE/ring in its epilogue: the scratch this call needs is checked
+    before any launch -- 0 bytes for 4096 rows x 32 heads (whole rounds of tiles) with aligned tables,
+    the whole [M, 3E] bf16 buffer with 8-byte aligned ones (unfused path) -- and a shape with a partial
+    last round needs it whatever the tables."""
+    p, p8 = ctypes.c_void_p(0x10000), ctypes.c_void_p(0x10008)
+    f = lib.joy_fp8_qkv_norm_rope_cache
+    size = lib.joy_fp8_qkv_norm_rope_cache_scratch_size
+
+    def call(M, cos=p, scratch=None, nbytes=0):
+        E = 32 * 128
+        return f(p, p, p, p, None, M, 1024, 32, 128, 1e-6, p, p, cos, cos, p, E, p, E, None, 0, None, None, 0, 0,
+                 0, 0, M, 0, scratch, nbytes, None)
+
+    assert size(4096, 1024, 32, 128) == 0 and size(4352, 1024, 32, 128) == 4352 * 3 * 4096 * 2
+    _status(lib, call(4096, cos=p8), 1, "bytes of scratch needed for this call")
+    _status(lib, call(4352), 1, "bytes of scratch needed for this call")
+    _status(lib, call(4352, scratch=p, nbytes=-1), 1, "scratch_bytes must be >= 0")
+
+
 def test_single_hip_runtime_in_process():
     """The library must bind to the HIP runtime torch already loaded (same SONAME),
     so its launches share torch's streams and queues."""

@@ -75,10 +75,20 @@ def _outputs(M, H, D, slots, cap, seed):
     return q, k, v, ck, cv
 
 
+def _shift_table(t, elems):
+    """The same table in a buffer whose first row starts `elems` elements past an aligned address."""
+    buf = torch.empty(t.numel() + elems, dtype=t.dtype, device=t.device)
+    view = buf[elems:].view(t.shape)
+    view.copy_(t)
+    return view
+
+
 def _run_both(M, K, H, D, seed, exact, cache_tokens=-1, pre_rope=True, with_q=True, with_k=True, with_v=True,
-              slot=1, offset=3):
+              slot=1, offset=3, table_shift=0):
     import joyomni_ops as jo
     a, b, sa, sw, bias, qw, kw, cos, sin = _problem(M, K, H, D, seed, exact)
+    if table_shift:
+        cos, sin = _shift_table(cos, table_shift), _shift_table(sin, table_shift)
     n = M if cache_tokens < 0 else cache_tokens
     slots, cap = 3, offset + M + 5
     ref = _outputs(M, H, D, slots, cap, seed + 1)
@@ -106,6 +116,7 @@ def u16_t(t):
     (777, 512, 5, 128),     # odd head count: fallback
     (300, 1024, 6, 64),     # head_dim 64: fallback
     (640, 640, 4, 128),     # K % 256 != 0: fallback
+    (1002, 1024, 8, 128),   # M % 4 != 0 (row scales read 4 at a time by the persistent kernel): fallback
 ])
 def test_exact_equals_gemm_then_norm_rope(M, K, H, D):
     announce("fp8 qkv norm rope exact", M, K, H, D)
@@ -133,3 +144,58 @@ def test_block_shape_random_operands():
     V tiles as quarter sub-tiles)."""
     announce("fp8 qkv norm rope block shape", 10800, 5120, 40, 128)
     _run_both(10800, 5120, 40, 128, 13, exact=False)
+
+
+@pytest.mark.parametrize("M", [4352, 4096])  # a partial last round; whole rounds (no scratch otherwise)
+def test_tables_not_16_byte_aligned(M):
+    """cos / sin rows that start 8 bytes past a 16-byte boundary: the torch op reads an aligned copy
+    (fused epilogue), the same bits as the two-op sequence."""
+    announce("fp8 qkv norm rope unaligned tables", M)
+    _run_both(M, 1024, 32, 128, 14, exact=True, table_shift=4)
+
+
+def test_capi_unaligned_tables_need_the_full_scratch():
+    """Through the C ABI, misaligned tables send the call to the unfused path, which needs the whole
+    [M, 3E] bf16 scratch even where the size query says 0 (4096 rows: whole rounds of tiles): with
+    no scratch the call fails before any launch and leaves the outputs alone; with M x 3E x 2 bytes
+    it gives the two-op sequence's bits."""
+    import joyomni_ops as jo
+    from joyomni_ops import _lib
+    announce("fp8 qkv norm rope C ABI unaligned tables")
+    M, K, H, D = 4096, 1024, 32, 128
+    N = 3 * H * D
+    a, b, sa, sw, bias, qw, kw, cos, sin = _problem(M, K, H, D, 16, exact=True)
+    cos, sin = _shift_table(cos, 4), _shift_table(sin, 4)
+    assert jo._LIB.joy_fp8_qkv_norm_rope_cache_scratch_size(M, K, H, D) == 0
+    slots, cap = 2, M
+    ref = _outputs(M, H, D, slots, cap, 17)
+    got = tuple(t.clone() for t in ref)
+    y = jo.fp8_scaled_mm(a, b, sa, sw, torch.bfloat16, bias)
+    jo.fused_qkv_norm_rope_cache(y, H, 1e-6, qw, kw, cos, sin, ref[0], ref[1], ref[3], ref[4], 1, 0, v_out=ref[2])
+    before = tuple(t.clone() for t in got)
+    st = torch.cuda.current_stream().cuda_stream
+
+    def call(scratch, nbytes):
+        return jo._LIB.joy_fp8_qkv_norm_rope_cache(
+            a.data_ptr(), b.data_ptr(), sa.data_ptr(), sw.data_ptr(), bias.data_ptr(), M, K, H, D, 1e-6,
+            qw.data_ptr(), kw.data_ptr(), cos.data_ptr(), sin.data_ptr(), got[0].data_ptr(), H * D,
+            got[1].data_ptr(), H * D, got[2].data_ptr(), H * D, got[3].data_ptr(), got[4].data_ptr(), slots, cap, 1,
+            0, M, 0, scratch, nbytes, st)
+
+    rc = call(None, 0)
+    assert rc == 1, rc  # JOY_ERR_INVALID_ARGUMENT
+    assert b"scratch needed for this call" in jo._LIB.joy_last_error()
+    torch.cuda.synchronize()
+    for r, o in zip(before, got):
+        assert torch.equal(u16_t(r), u16_t(o)), "outputs written by a refused call"
+    scratch = torch.empty(M * N * 2, dtype=torch.uint8, device=DEV)
+    _lib.check(jo._LIB, call(scratch.data_ptr(), scratch.numel()))
+    torch.cuda.synchronize()
+    for name, r, o in zip(("q_out", "k_out", "v_out", "ring K", "ring V"), ref, got):
+        assert torch.equal(u16_t(r), u16_t(o)), f"{name} differs"
+
+
+def test_no_ring_rows_written():
+    """cache_tokens = 0: the ring keeps every row; Q / K / V are still written."""
+    announce("fp8 qkv norm rope no ring rows")
+    _run_both(4352, 1024, 32, 128, 15, exact=True, cache_tokens=0)
