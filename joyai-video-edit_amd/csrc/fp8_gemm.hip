@@ -18,6 +18,8 @@
 //    16x16x128 MFMAs;
 //  * fp8_gemm_4k (M <= 512, and long-K GEMMs of less than one round): deep-K tiles
 //    with register-staged operands and optional split-K;
+//  * fp8_gemm_4n (129-512 rows with N % 80 == 0, e.g. N 5120): one round of narrow
+//    BM x 80 tiles, no K split;
 //  * fp8_gemm_4h (K % 128 == 0): one 256x128 or 128x128 tile per workgroup with the
 //    persistent kernel's 128-byte K steps; the sub-tiles of the last, partial round and
 //    single-round GEMMs of <= 2048 rows that 256x128 tiles fill best;
