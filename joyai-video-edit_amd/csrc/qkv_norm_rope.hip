@@ -147,11 +147,14 @@ __global__ __launch_bounds__(512) void qk_norm_rope_kernel(NormRopeArgs a) {
   }
 }
 
-// Launch: one (token, head) group per wave (UPT = 1), non-temporal traffic, 8 waves
-// per workgroup -- the best of the shapes measured on MI355X for L = 10800, H = 40.
+// Launch: two (token, head) groups per wave (UPT = 2), non-temporal traffic, 4 waves per
+// workgroup. Measured on four MI355X boxes at L = 10800, H = 40 against one group per wave and
+// 8 waves per workgroup (graph-replayed, same-process A/B, bit-identical): 127.9 / 134.1 / 126.9 /
+// 127.0 us against 132.4 / 133.9 / 131.2 / 131.8; four or more groups per wave were faster on one
+// box only (UPT 4: 128.5-129.6 / 129.4-130.4 / 129.6-129.8 us), eight slower everywhere.
 template <int D>
 hipError_t launch_norm_rope_d(const NormRopeArgs& a, hipStream_t st) {
-  constexpr int UPT = 1, WPB = 8;
+  constexpr int UPT = 2, WPB = 4;
   constexpr int HPW = kWave / (D / 8);
   const int64_t units = a.n_tokens * a.num_heads;
   const int64_t waves = (units + HPW * UPT - 1) / (HPW * UPT);
