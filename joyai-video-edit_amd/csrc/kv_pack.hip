@@ -89,69 +89,80 @@ __device__ __forceinline__ const uint16_t* row_ptr(const RowView& v, int64_t row
   return v.ptr + t * v.stride_token + h * v.stride_head;
 }
 
-template <bool VEC>
+// U groups of kRPW consecutive rows per wave: every lane issues its U loads before any
+// arithmetic (one row per 16-lane group left each lane a single 16-byte load in flight).
+template <bool VEC, int U>
 __global__ __launch_bounds__(kWPB * kWave) void joint_qkv_pack_kernel(JointPackArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
   const int li = lane % kLPR;
-  const int64_t row =
-      ((int64_t)blockIdx.x * kWPB + (threadIdx.x >> 6)) * kRPW + lane / kLPR;
+  const int64_t row0 = ((int64_t)blockIdx.x * kWPB + (threadIdx.x >> 6)) * U * kRPW + lane / kLPR;
   const int64_t img_rows = a.img_len * a.heads;
   const int64_t txt_rows = a.txt_len * a.heads;
   const int64_t cache_rows = a.cache_len * a.heads;
   const int64_t q_rows = img_rows + txt_rows;
   const int64_t kv_rows = cache_rows + q_rows;
-  const bool valid = row < q_rows + 2 * kv_rows;
 
-  // Source row, destination row and (for text Q/K) the norm weight of this row.
-  RowView src;
-  int64_t srow;
-  uint16_t* dst;
-  const uint16_t* w = nullptr;
-  if (row < q_rows) {
-    dst = a.out_q + row * kD;
-    if (row < img_rows) {
-      src = a.img_q;
-      srow = row;
-    } else {
-      src = a.txt_q;
-      srow = row - img_rows;
-      w = a.txt_q_weight;
-    }
-  } else {
-    const bool is_v = row >= q_rows + kv_rows;
-    const int64_t kv = is_v ? row - q_rows - kv_rows : row - q_rows;
-    dst = (is_v ? a.out_v : a.out_k) + kv * kD;
-    if (kv < cache_rows) {
-      src = is_v ? a.cache_v : a.cache_k;
-      srow = kv;
-    } else if (kv < cache_rows + img_rows) {
-      src = is_v ? a.img_v : a.img_k;
-      srow = kv - cache_rows;
-    } else {
-      src = is_v ? a.txt_v : a.txt_k;
-      srow = kv - cache_rows - img_rows;
-      if (!is_v) w = a.txt_k_weight;
-    }
-  }
-
-  uint4 x = make_uint4(0, 0, 0, 0);
-  if (valid) x = load8<VEC>(row_ptr(src, srow, a.heads) + li * 8);
-  float f[8];
-  unpack8(x, f);
-  float ss = 0.f;
+  uint4 x[U];
+  uint16_t* dst[U];
+  const uint16_t* w[U];
+  bool valid[U];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) ss = __builtin_fmaf(f[j], f[j], ss);
-  ss = row_sum(ss);  // every lane takes part, whatever its row needs
-  if (!valid) return;
-  if (w) {
-    const float r = __builtin_amdgcn_rsqf(ss * (1.0f / kD) + a.eps);
-    float wf[8];
-    unpack8(load8<VEC>(w + li * 8), wf);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) f[j] = bf16_round(f[j] * r) * wf[j];
-    x = pack8(f);
+  for (int u = 0; u < U; ++u) {
+    const int64_t row = row0 + u * kRPW;
+    valid[u] = row < q_rows + 2 * kv_rows;
+    // source row, destination row and (for text Q/K) the norm weight of this row
+    RowView src;
+    int64_t srow;
+    w[u] = nullptr;
+    if (row < q_rows) {
+      dst[u] = a.out_q + row * kD;
+      if (row < img_rows) {
+        src = a.img_q;
+        srow = row;
+      } else {
+        src = a.txt_q;
+        srow = row - img_rows;
+        w[u] = a.txt_q_weight;
+      }
+    } else {
+      const bool is_v = row >= q_rows + kv_rows;
+      const int64_t kv = is_v ? row - q_rows - kv_rows : row - q_rows;
+      dst[u] = (is_v ? a.out_v : a.out_k) + kv * kD;
+      if (kv < cache_rows) {
+        src = is_v ? a.cache_v : a.cache_k;
+        srow = kv;
+      } else if (kv < cache_rows + img_rows) {
+        src = is_v ? a.img_v : a.img_k;
+        srow = kv - cache_rows;
+      } else {
+        src = is_v ? a.txt_v : a.txt_k;
+        srow = kv - cache_rows - img_rows;
+        if (!is_v) w[u] = a.txt_k_weight;
+      }
+    }
+    x[u] = make_uint4(0, 0, 0, 0);
+    if (valid[u]) x[u] = load8<VEC>(row_ptr(src, srow, a.heads) + li * 8);
   }
-  store8<VEC>(dst + li * 8, x);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    float f[8];
+    unpack8(x[u], f);
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss = __builtin_fmaf(f[j], f[j], ss);
+    ss = row_sum(ss);  // every lane takes part, whatever its row needs
+    if (!valid[u]) continue;
+    uint4 y = x[u];
+    if (w[u]) {
+      const float r = __builtin_amdgcn_rsqf(ss * (1.0f / kD) + a.eps);
+      float wf[8];
+      unpack8(load8<VEC>(w[u] + li * 8), wf);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) f[j] = bf16_round(f[j] * r) * wf[j];
+      y = pack8(f);
+    }
+    store8<VEC>(dst[u] + li * 8, y);
+  }
 }
 
 // One 16-lane group per (token, group of kHPG heads): the token's cos/sin entries
@@ -240,10 +251,13 @@ hipError_t launch_joint_qkv_pack(const JointPackArgs& a, hipStream_t st) {
                    (uintptr_t)a.txt_q_weight % 16 == 0 && (uintptr_t)a.txt_k_weight % 16 == 0 &&
                    (uintptr_t)a.out_q % 16 == 0 && (uintptr_t)a.out_k % 16 == 0 &&
                    (uintptr_t)a.out_v % 16 == 0;
+  // two row groups per wave: 347 -> 330 us at 32400 cached + 10800 + 512 tokens (four: no further gain)
+  constexpr int U = 2;
+  const dim3 grid((unsigned)((rows + (int64_t)kWPB * kRPW * U - 1) / ((int64_t)kWPB * kRPW * U)));
   if (vec)
-    hipLaunchKernelGGL(joint_qkv_pack_kernel<true>, grid_for_rows(rows), dim3(kWPB * kWave), 0, st, a);
+    hipLaunchKernelGGL((joint_qkv_pack_kernel<true, U>), grid, dim3(kWPB * kWave), 0, st, a);
   else
-    hipLaunchKernelGGL(joint_qkv_pack_kernel<false>, grid_for_rows(rows), dim3(kWPB * kWave), 0, st, a);
+    hipLaunchKernelGGL((joint_qkv_pack_kernel<false, U>), grid, dim3(kWPB * kWave), 0, st, a);
   return hipGetLastError();
 }
 
