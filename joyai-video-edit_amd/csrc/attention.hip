@@ -15,7 +15,9 @@
 //   * S^T = K Q^T: 8 v_mfma_f32_32x32x16_bf16 (K from LDS as the A operand, the wave's 32
 //     queries kept in registers as the B operand). In the 32x32 output a lane holds 16 keys of
 //     ONE query, so the row max / row sum are in-lane plus one exchange with lane ^ 32;
-//   * online softmax in fp32 with exp2 (scale * log2 e folded into the scores);
+//   * online softmax in fp32 with exp2 (scale * log2 e folded into the scores), computed first
+//     against the running max and redone with the half's row max only when a probability could
+//     reach 2^7 (the first tile, or a new maximum);
 //   * O^T += V^T P^T: 8 MFMAs; P^T is the B operand straight from the registers that hold the
 //     scores (rounded to bf16), which fixes a permutation of the 16 keys of each MFMA; the A
 //     operand (V^T) comes from the key-major V tile with two ds_read_b64_tr_b16 per MFMA, whose
@@ -177,48 +179,60 @@ __global__ __launch_bounds__(64 * kWaves, 1) void attn_fwd_d128(AttnArgs a, int 
   float m_run = -INFINITY, l_run = 0.f;
   const float sl2 = a.scale_log2e;
 
-  // softmax of one 32-key half (16 scores per lane) in 8 steps
+  // Softmax of one 32-key half (16 scores per lane), first against the running max m_run: steps 0-3
+  // compute 4 probabilities each, rounded to bf16 pairs for the PV operand and summed as those bf16
+  // values (v_dot2c_f32_bf16 against (1, 1)), so the row sum normalises exactly the weights the MFMAs
+  // apply; step 4 completes the row sum over the 32 keys. If every query's sum is below 2^7, every
+  // probability is, so no score exceeds m_run by kMaxSlack (log2 units) and the max-based step below
+  // (soft_max) would keep m_new = m_run and compute the same values: the half needs no row max. Else
+  // (the first tile, where m_run = -inf, or a new maximum) the wave redoes the half with soft_max.
   struct Soft {
-    float m, m_new, alpha, rs;
+    float m_new, alpha, rs;
+    bool ok;
+  };
+  auto probs = [&](int r0, const v16f& s, v4i (&pb)[2], float m_ref, float& rs) {
+    float q[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) q[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r0 + j], sl2, -m_ref));
+    const uint32_t pk0 = pack_bf16x2(q[0], q[1]), pk1 = pack_bf16x2(q[2], q[3]);
+    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+    rs = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk0), one, rs, false);
+    rs = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk1), one, rs, false);
+    const int h = (r0 >> 2) & 1;
+    pb[r0 >> 3][2 * h] = (int)pk0;
+    pb[r0 >> 3][2 * h + 1] = (int)pk1;
   };
   auto soft_step = [&](int step, const v16f& s, v4i (&pb)[2], Soft& st) {
-    if (step == 0) {  // max of 16 scores as a chain of 3-input maxima (v_max3_f32)
-      float m = fmaxf(fmaxf(s[0], s[1]), s[2]);
-#pragma unroll
-      for (int r = 3; r < 9; r += 2) m = fmaxf(fmaxf(m, s[r]), s[r + 1]);
-      st.m = m;
-    } else if (step == 1) {
-      float m = st.m;
-#pragma unroll
-      for (int r = 9; r < 15; r += 2) m = fmaxf(fmaxf(m, s[r]), s[r + 1]);
-      const float mt = xor32_max(fmaxf(m, s[15]));
-      // the running max moves only when a score exceeds it by more than kMaxSlack (log2 units):
-      // probabilities then stay below 2^kMaxSlack, and the rescale of O is rare after the first
-      // tiles (the first tile always sets it: m_run starts at -inf)
-      const float m_cand = mt * sl2;
-      st.m_new = m_cand - m_run > kMaxSlack ? m_cand : m_run;
-      st.alpha = __builtin_amdgcn_exp2f(m_run - st.m_new);
-      st.rs = 0.f;
-    } else if (step <= 5) {
-      // 4 probabilities: rounded to bf16 pairs for the PV operand, and summed as those bf16 values
-      // (two v_dot2c_f32_bf16 against (1, 1)), so the row sum normalises exactly the weights the
-      // MFMAs apply
-      const int r0 = (step - 2) * 4;
-      float q[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) q[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r0 + j], sl2, -st.m_new));
-      const uint32_t pk0 = pack_bf16x2(q[0], q[1]), pk1 = pack_bf16x2(q[2], q[3]);
-      const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
-      st.rs = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk0), one, st.rs, false);
-      st.rs = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk1), one, st.rs, false);
-      const int h = (r0 >> 2) & 1;
-      pb[r0 >> 3][2 * h] = (int)pk0;
-      pb[r0 >> 3][2 * h + 1] = (int)pk1;
-    } else if (step == 6) {
+    if (step == 0) st.rs = 0.f;
+    if (step <= 3) {
+      probs(step * 4, s, pb, m_run, st.rs);
+    } else if (step == 4) {
       st.rs = xor32_sum(st.rs);
-      l_run = l_run * st.alpha + st.rs;
-      m_run = st.m_new;
+      st.ok = st.rs < 128.0f;  // false for inf / NaN (m_run = -inf)
+      st.m_new = m_run;
+      st.alpha = 1.0f;
     }
+  };
+  // the same half with its row max: the running max moves only when a score exceeds it by more than
+  // kMaxSlack, so probabilities stay below 2^kMaxSlack and the rescale of O is rare after the first
+  // tiles (the first tile always sets it: m_run starts at -inf)
+  auto soft_max = [&](const v16f& s, v4i (&pb)[2], Soft& st) {
+    float m = fmaxf(fmaxf(s[0], s[1]), s[2]);
+#pragma unroll
+    for (int r = 3; r < 15; r += 2) m = fmaxf(fmaxf(m, s[r]), s[r + 1]);
+    const float mt = xor32_max(fmaxf(m, s[15]));
+    const float m_cand = mt * sl2;
+    st.m_new = m_cand - m_run > kMaxSlack ? m_cand : m_run;
+    st.alpha = __builtin_amdgcn_exp2f(m_run - st.m_new);
+    st.rs = 0.f;
+#pragma unroll
+    for (int step = 0; step < 4; ++step) probs(step * 4, s, pb, st.m_new, st.rs);
+    st.rs = xor32_sum(st.rs);
+  };
+  auto soft_end = [&](const v16f& s, v4i (&pb)[2], Soft& st) {
+    if (__builtin_amdgcn_ballot_w64(!st.ok) != 0) soft_max(s, pb, st);
+    l_run = l_run * st.alpha + st.rs;
+    m_run = st.m_new;
   };
   auto rescale = [&](float alpha) {
     if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
@@ -296,10 +310,12 @@ __global__ __launch_bounds__(64 * kWaves, 1) void attn_fwd_d128(AttnArgs a, int 
         if constexpr (partial) mask(s0, 0);
         __builtin_amdgcn_sched_barrier(0);
       } else if (i == 15) {
+        soft_end(s0, p0, st0);
         rescale(st0.alpha);
         if constexpr (partial) mask(s1, 1);
         __builtin_amdgcn_sched_barrier(0);
       } else if (i == 23) {
+        soft_end(s1, p1, st1);
         rescale(st1.alpha);
         __builtin_amdgcn_sched_barrier(0);
       }
