@@ -179,39 +179,29 @@ __global__ __launch_bounds__(64 * kWaves, 1) void attn_fwd_d128(AttnArgs a, int 
   float m_run = -INFINITY, l_run = 0.f;
   const float sl2 = a.scale_log2e;
 
-  // Softmax of one 32-key half (16 scores per lane), first against the running max m_run: steps 0-3
-  // compute 4 probabilities each, rounded to bf16 pairs for the PV operand and summed as those bf16
-  // values (v_dot2c_f32_bf16 against (1, 1)), so the row sum normalises exactly the weights the MFMAs
-  // apply; step 4 completes the row sum over the 32 keys. If every query's sum is below 2^7, every
-  // probability is, so no score exceeds m_run by kMaxSlack (log2 units) and the max-based step below
-  // (soft_max) would keep m_new = m_run and compute the same values: the half needs no row max. Else
-  // (the first tile, where m_run = -inf, or a new maximum) the wave redoes the half with soft_max.
+  // Softmax of one 32-key half (16 scores per lane), first against the running max m_run: steps 0-7
+  // (one after each MFMA of the phase) compute 2 probabilities each, rounded to a bf16 pair for the
+  // PV operand and summed as those bf16 values (v_dot2c_f32_bf16 against (1, 1)), so the row sum
+  // normalises exactly the weights the MFMAs apply; soft_end completes the row sum over the 32 keys.
+  // If every query's sum is below 2^7, every probability is, so no score exceeds m_run by kMaxSlack
+  // (log2 units) and the max-based form below (soft_max) would keep m_new = m_run and compute the
+  // same values: the half needs no row max. Else (the first tile, where m_run = -inf, or a new
+  // maximum) the wave redoes the half with soft_max.
   struct Soft {
     float m_new, alpha, rs;
-    bool ok;
   };
-  auto probs = [&](int r0, const v16f& s, v4i (&pb)[2], float m_ref, float& rs) {
-    float q[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) q[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r0 + j], sl2, -m_ref));
-    const uint32_t pk0 = pack_bf16x2(q[0], q[1]), pk1 = pack_bf16x2(q[2], q[3]);
-    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
-    rs = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk0), one, rs, false);
-    rs = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk1), one, rs, false);
-    const int h = (r0 >> 2) & 1;
-    pb[r0 >> 3][2 * h] = (int)pk0;
-    pb[r0 >> 3][2 * h + 1] = (int)pk1;
+  const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+  // probabilities 2 e and 2 e + 1 against m_ref
+  auto probs = [&](int e, const v16f& s, v4i (&pb)[2], float m_ref, float& rs) {
+    const float q0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * e], sl2, -m_ref));
+    const float q1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * e + 1], sl2, -m_ref));
+    const uint32_t pk = pack_bf16x2(q0, q1);
+    rs = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk), one, rs, false);
+    pb[e >> 2][e & 3] = (int)pk;
   };
   auto soft_step = [&](int step, const v16f& s, v4i (&pb)[2], Soft& st) {
     if (step == 0) st.rs = 0.f;
-    if (step <= 3) {
-      probs(step * 4, s, pb, m_run, st.rs);
-    } else if (step == 4) {
-      st.rs = xor32_sum(st.rs);
-      st.ok = st.rs < 128.0f;  // false for inf / NaN (m_run = -inf)
-      st.m_new = m_run;
-      st.alpha = 1.0f;
-    }
+    probs(step, s, pb, m_run, st.rs);
   };
   // the same half with its row max: the running max moves only when a score exceeds it by more than
   // kMaxSlack, so probabilities stay below 2^kMaxSlack and the rescale of O is rare after the first
@@ -226,11 +216,15 @@ __global__ __launch_bounds__(64 * kWaves, 1) void attn_fwd_d128(AttnArgs a, int 
     st.alpha = __builtin_amdgcn_exp2f(m_run - st.m_new);
     st.rs = 0.f;
 #pragma unroll
-    for (int step = 0; step < 4; ++step) probs(step * 4, s, pb, st.m_new, st.rs);
+    for (int e = 0; e < 8; ++e) probs(e, s, pb, st.m_new, st.rs);
     st.rs = xor32_sum(st.rs);
   };
   auto soft_end = [&](const v16f& s, v4i (&pb)[2], Soft& st) {
-    if (__builtin_amdgcn_ballot_w64(!st.ok) != 0) soft_max(s, pb, st);
+    st.rs = xor32_sum(st.rs);
+    st.m_new = m_run;
+    st.alpha = 1.0f;
+    // false for inf / NaN (m_run = -inf)
+    if (__builtin_amdgcn_ballot_w64(!(st.rs < 128.0f)) != 0) soft_max(s, pb, st);
     l_run = l_run * st.alpha + st.rs;
     m_run = st.m_new;
   };
