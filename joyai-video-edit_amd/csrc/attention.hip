@@ -292,9 +292,11 @@ __global__ __launch_bounds__(64 * kWaves, 1) void attn_fwd_d128(AttnArgs a, int 
         s0 = mfma_bf16(as_bf16x8(op), as_bf16x8(qf[i]), i == 0 ? (v16f){} : s0);
       } else if (i < 16) {  // S(1) with softmax(0)
         s1 = mfma_bf16(as_bf16x8(op), as_bf16x8(qf[i - 8]), i == 8 ? (v16f){} : s1);
+        __builtin_amdgcn_sched_barrier(0);
         soft_step(i - 8, s0, p0, st0);
       } else if (i < 24) {  // PV(0) with softmax(1)
         o[(i - 16) & 3] = mfma_bf16(as_bf16x8(op), as_bf16x8(p0[(i - 16) >> 2]), o[(i - 16) & 3]);
+        __builtin_amdgcn_sched_barrier(0);
         soft_step(i - 16, s1, p1, st1);
       } else {  // PV(1)
         o[(i - 24) & 3] = mfma_bf16(as_bf16x8(op), as_bf16x8(p1[(i - 24) >> 2]), o[(i - 24) & 3]);
