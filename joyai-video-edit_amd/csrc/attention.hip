@@ -182,8 +182,8 @@ __global__ __launch_bounds__(64 * kWaves, 1) void attn_fwd_d128(AttnArgs a, int 
   // Softmax of one 32-key half (16 scores per lane), first against the running max m_run: steps 0-7
   // (one after each MFMA of the phase) compute 2 probabilities each, rounded to a bf16 pair for the
   // PV operand and summed as those bf16 values (v_dot2c_f32_bf16 against (1, 1)), so the row sum
-  // normalises exactly the weights the MFMAs apply; soft_end completes the row sum over the 32 keys.
-  // If every query's sum is below 2^7, every probability is, so no score exceeds m_run by kMaxSlack
+  // normalises exactly the weights the MFMAs apply. If every lane's sum (16 keys of a query) is below
+  // 2^7, every probability is, so no score exceeds m_run by kMaxSlack
   // (log2 units) and the max-based form below (soft_max) would keep m_new = m_run and compute the
   // same values: the half needs no row max. Else (the first tile, where m_run = -inf, or a new
   // maximum) the wave redoes the half with soft_max.
@@ -217,17 +217,18 @@ __global__ __launch_bounds__(64 * kWaves, 1) void attn_fwd_d128(AttnArgs a, int 
     st.rs = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) probs(e, s, pb, st.m_new, st.rs);
-    st.rs = xor32_sum(st.rs);
   };
+  // Before the half's PV MFMAs: the check, on each lane's 16 keys (a sum below 2^7 there bounds every
+  // probability as well), and the max-based redo where it fails. The row sum over the 32 keys and
+  // the running sum follow after the first PV MFMA (soft_sum).
   auto soft_end = [&](const v16f& s, v4i (&pb)[2], Soft& st) {
-    st.rs = xor32_sum(st.rs);
     st.m_new = m_run;
     st.alpha = 1.0f;
     // false for inf / NaN (m_run = -inf)
     if (__builtin_amdgcn_ballot_w64(!(st.rs < 128.0f)) != 0) soft_max(s, pb, st);
-    l_run = l_run * st.alpha + st.rs;
     m_run = st.m_new;
   };
+  auto soft_sum = [&](Soft& st) { l_run = l_run * st.alpha + xor32_sum(st.rs); };
   auto rescale = [&](float alpha) {
     if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
@@ -297,9 +298,14 @@ __global__ __launch_bounds__(64 * kWaves, 1) void attn_fwd_d128(AttnArgs a, int 
       } else if (i < 24) {  // PV(0) with softmax(1)
         o[(i - 16) & 3] = mfma_bf16(as_bf16x8(op), as_bf16x8(p0[(i - 16) >> 2]), o[(i - 16) & 3]);
         __builtin_amdgcn_sched_barrier(0);
+        if (i == 16) soft_sum(st0);
         soft_step(i - 16, s1, p1, st1);
       } else {  // PV(1)
         o[(i - 24) & 3] = mfma_bf16(as_bf16x8(op), as_bf16x8(p1[(i - 24) >> 2]), o[(i - 24) & 3]);
+        if (i == 24) {
+          __builtin_amdgcn_sched_barrier(0);
+          soft_sum(st1);
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
       if (i == 7) {
