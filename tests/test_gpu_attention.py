@@ -69,6 +69,34 @@ def test_peaked_scores_and_explicit_scale():
     _check(_run(q, k, v, 0.02), q, k, v, "scale 0.02", scale=0.02)
 
 
+def test_running_max_jumps_across_tiles():
+    """Scores that jump between 64-key tiles, so that the softmax's first pass against the running
+    max fails its check and the max-based pass takes over in every way it can: a jump of about 5
+    and 7.9 (log2 units, below the slack of 8: the sum check fails, the running max stays), of
+    about 12.7 (the running max moves and O is rescaled), a drop of about 20 (tiny probabilities,
+    the first pass holds) and of about 200 (probabilities against the old max overflow to inf).
+    Key rows carry their level in dimension 0 and queries 4 there, on top of small random parts;
+    the last tile is partial (17 keys)."""
+    announce("attention running-max jumps")
+    g = gen(41)
+    Lq, H, tiles = 96, 2, 11
+    Lk = 64 * (tiles - 1) + 17
+    q = torch.randn(Lq, H, 128, generator=g) * 0.1
+    k = torch.randn(Lk, H, 128, generator=g) * 0.1
+    v = torch.randn(Lk, H, 128, generator=g)
+    q[:, :, 0] = 4.0
+    # level of dimension 0 per tile: scores move by 4 * level / sqrt(128) * log2(e) ~ 0.51 * level
+    levels = {0: 0.0, 3: 10.0, 4: 15.5, 6: 25.0, 7: -40.0, 8: 400.0, 9: 0.0, 10: 401.0}
+    for t, lv in levels.items():
+        rows = slice(64 * t, min(64 * (t + 1), Lk))
+        k[rows, 0, 0] = lv
+        k[rows, 1, 0] = -lv if t in (3, 7) else lv  # head 1: drops where head 0 jumps
+    q, k, v = q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
+    out = _run(q, k, v)
+    assert torch.isfinite(out.float()).all()
+    _check(out, q, k, v, "running-max jumps")
+
+
 def test_single_key_is_exact():
     announce("attention single key")
     q, k, v = _inputs(77, 1, 3, 11)
