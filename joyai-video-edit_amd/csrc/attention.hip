@@ -363,7 +363,10 @@ __global__ __launch_bounds__(64 * kWaves, 1) void attn_fwd_d128(AttnArgs a, int 
 // waves per workgroup it spills to scratch), and the same kernel without the half-tile split
 // (MFMA busy 49 % at 1.94 GHz against 54 % at 1.83 GHz here: the part is power-limited, so the
 // better overlap buys 2.6 %). A three-stage K / V ring (next-but-one tile in flight) measured no
-// faster than two stages.
+// faster than two stages. Two query blocks per wave at one wave per SIMD with the output
+// accumulators pinned in a0..a127 by inline asm (no accumulator copies, no spills, bit-identical):
+// 3-5 % slower than this kernel -- half the LDS operand reads and a higher clock (2.1 against
+// 1.87 GHz), but the single wave's own latencies exposed (MFMA busy 0.47 against 0.55).
 hipError_t launch_attention_fwd(const AttnArgs& a, hipStream_t st) {
   // query blocks per head: at least kWaves, so a workgroup spans at most two heads
   const int qb = (int)max((a.q_len + 31) / 32, (int64_t)kWaves);
