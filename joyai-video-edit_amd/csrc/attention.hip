@@ -17,7 +17,7 @@
 //     ONE query, so the row max / row sum are in-lane plus one exchange with lane ^ 32;
 //   * online softmax in fp32 with exp2 (scale * log2 e folded into the scores), computed first
 //     against the running max and redone with the half's row max only when a probability could
-//     reach 2^7 (the first tile, or a new maximum);
+//     reach 2^7 (the first tile, or scores well above the running max);
 //   * O^T += V^T P^T: 8 MFMAs; P^T is the B operand straight from the registers that hold the
 //     scores (rounded to bf16), which fixes a permutation of the 16 keys of each MFMA; the A
 //     operand (V^T) comes from the key-major V tile with two ds_read_b64_tr_b16 per MFMA, whose
@@ -48,7 +48,6 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kD = 128;
-constexpr float kMaxSlack = 8.0f;  // see soft_step
 constexpr int kBK = 64;                // keys per tile
 constexpr int kRowB = kD * 2;          // bytes per K / V row
 constexpr int kTileB = kBK * kRowB;    // 16 KB per K or V tile
@@ -182,11 +181,11 @@ __global__ __launch_bounds__(64 * kWaves, 1) void attn_fwd_d128(AttnArgs a, int 
   // Softmax of one 32-key half (16 scores per lane), first against the running max m_run: steps 0-7
   // (one after each MFMA of the phase) compute 2 probabilities each, rounded to a bf16 pair for the
   // PV operand and summed as those bf16 values (v_dot2c_f32_bf16 against (1, 1)), so the row sum
-  // normalises exactly the weights the MFMAs apply. If every lane's sum (16 keys of a query) is below
-  // 2^7, every probability is, so no score exceeds m_run by kMaxSlack
-  // (log2 units) and the max-based form below (soft_max) would keep m_new = m_run and compute the
-  // same values: the half needs no row max. Else (the first tile, where m_run = -inf, or a new
-  // maximum) the wave redoes the half with soft_max.
+  // normalises exactly the weights the MFMAs apply. The online softmax is exact for any reference
+  // point, so the half needs no row max as long as its probabilities stay small: if every lane's sum
+  // (16 keys of a query) is below 2^7, every probability is, and the half is done. Else (the first
+  // tile, where m_run = -inf, or scores well above m_run) the wave redoes the half against the
+  // larger of m_run and its row max (soft_max), and O is rescaled.
   struct Soft {
     float m_new, alpha, rs;
   };
@@ -203,16 +202,15 @@ __global__ __launch_bounds__(64 * kWaves, 1) void attn_fwd_d128(AttnArgs a, int 
     if (step == 0) st.rs = 0.f;
     probs(step, s, pb, m_run, st.rs);
   };
-  // the same half with its row max: the running max moves only when a score exceeds it by more than
-  // kMaxSlack, so probabilities stay below 2^kMaxSlack and the rescale of O is rare after the first
-  // tiles (the first tile always sets it: m_run starts at -inf)
+  // the same half against max(m_run, row max): its probabilities are then at most 1, and the later
+  // halves pass the check unless their scores rise again
   auto soft_max = [&](const v16f& s, v4i (&pb)[2], Soft& st) {
     float m = fmaxf(fmaxf(s[0], s[1]), s[2]);
 #pragma unroll
     for (int r = 3; r < 15; r += 2) m = fmaxf(fmaxf(m, s[r]), s[r + 1]);
     const float mt = xor32_max(fmaxf(m, s[15]));
     const float m_cand = mt * sl2;
-    st.m_new = m_cand - m_run > kMaxSlack ? m_cand : m_run;
+    st.m_new = fmaxf(m_run, m_cand);
     st.alpha = __builtin_amdgcn_exp2f(m_run - st.m_new);
     st.rs = 0.f;
 #pragma unroll
