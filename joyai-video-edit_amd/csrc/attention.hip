@@ -216,23 +216,26 @@ __global__ __launch_bounds__(64 * kWaves, 1) void attn_fwd_d128(AttnArgs a, int 
 #pragma unroll
     for (int e = 0; e < 8; ++e) probs(e, s, pb, st.m_new, st.rs);
   };
-  // Before the half's PV MFMAs: the check, on each lane's 16 keys (a sum below 2^7 there bounds every
-  // probability as well), and the max-based redo where it fails. The row sum over the 32 keys and
-  // the running sum follow after the first PV MFMA (soft_sum).
-  auto soft_end = [&](const v16f& s, v4i (&pb)[2], Soft& st) {
-    st.m_new = m_run;
-    st.alpha = 1.0f;
-    // false for inf / NaN (m_run = -inf)
-    if (__builtin_amdgcn_ballot_w64(!(st.rs < 128.0f)) != 0) soft_max(s, pb, st);
-    m_run = st.m_new;
-  };
-  auto soft_sum = [&](Soft& st) { l_run = l_run * st.alpha + xor32_sum(st.rs); };
   auto rescale = [&](float alpha) {
     if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
       for (int db = 0; db < 4; ++db) o[db] *= alpha;
     }
   };
+  // Before the half's PV MFMAs: the check, on each lane's 16 keys (a sum below 2^7 there bounds every
+  // probability as well), and where it fails the max-based redo and the rescale of O (the rare path,
+  // laid out off the fall-through). The row sum over the 32 keys and the running sum follow after the
+  // first PV MFMA (soft_sum).
+  auto soft_end = [&](const v16f& s, v4i (&pb)[2], Soft& st) {
+    st.alpha = 1.0f;
+    // false for inf / NaN (m_run = -inf)
+    if (__builtin_expect(__builtin_amdgcn_ballot_w64(!(st.rs < 128.0f)) != 0, 0)) {
+      soft_max(s, pb, st);
+      m_run = st.m_new;
+      rescale(st.alpha);
+    }
+  };
+  auto soft_sum = [&](Soft& st) { l_run = l_run * st.alpha + xor32_sum(st.rs); };
   auto k_operand = [&](const uint8_t* kt, int kb, int st) -> v4i {
     return *(const v4i*)(kt + chunk_at(kb * 32 + ql, 2 * st + hf));
   };
@@ -311,12 +314,10 @@ __global__ __launch_bounds__(64 * kWaves, 1) void attn_fwd_d128(AttnArgs a, int 
         __builtin_amdgcn_sched_barrier(0);
       } else if (i == 15) {
         soft_end(s0, p0, st0);
-        rescale(st0.alpha);
         if constexpr (partial) mask(s1, 1);
         __builtin_amdgcn_sched_barrier(0);
       } else if (i == 23) {
         soft_end(s1, p1, st1);
-        rescale(st1.alpha);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
