@@ -311,6 +311,57 @@ def test_block_joint_kv_reuses_cached_rows():
     assert same(fwd(joint), ref3)
 
 
+def test_block_hip_graph_replay_matches_eager():
+    """One block call (both HIP streams, the joint K / V reused from a JointKV) captured in a HIP
+    graph, as a serving loop would replay it in place of a tracing compiler: every replay gives the
+    eager call's bits, with eager calls between the replays, and a replay after new inputs are
+    written into the captured input tensors gives the eager result on those inputs."""
+    from joyomni_ops.dit_block import CachedChunk, JointKV, KVRing
+    announce("block HIP graph replay")
+    g, blk, img, txt, vec = _small_block(88)
+    L, H, D = img.shape[1], 4, 128
+    cos_h, sin_h = (t.to(DEV) for t in _half_tables([2], 12, 20))
+    cf, sf = (t.to(DEV) for t in _full_tables([0, 1], 12, 20))
+    ring = KVRing(4, L, H, D, DEV)
+    for slot in (2, 3):
+        ring.k[slot].copy_(torch.randn(L, H, D, generator=g).to(torch.bfloat16))
+        ring.v[slot].copy_(torch.randn(L, H, D, generator=g).to(torch.bfloat16))
+        ring.lengths[slot] = L
+    cached = [CachedChunk(2, cf[:L], sf[:L]), CachedChunk(3, cf[L:], sf[L:])]
+    img_d, txt_d, vec_d = img.to(DEV), txt.to(DEV), vec.to(DEV)
+    joint = JointKV()
+
+    def fwd():
+        return blk.forward(img_d, txt_d, vec_d, cos_h, sin_h, ring=ring, write_slot=0, cached=cached, joint=joint)
+
+    def bits(outs):
+        return [t.clone().view(torch.int16) for t in (*outs, ring.k[0], ring.v[0])]
+
+    ref = bits(fwd())
+    fwd()
+    torch.cuda.synchronize()
+    graph, cap = torch.cuda.CUDAGraph(), torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap):
+        with torch.cuda.graph(graph, stream=cap):
+            outs = fwd()
+    torch.cuda.synchronize()
+    for r in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        got = bits(outs)
+        assert all(torch.equal(a, b) for a, b in zip(got, ref)), f"replay {r} differs from the eager call"
+        assert all(torch.equal(a, b) for a, b in zip(bits(fwd()), ref)), f"eager call after replay {r} differs"
+    img_d.copy_(torch.randn(img_d.shape, generator=g).to(torch.bfloat16))
+    vec_d.copy_(torch.randn(vec_d.shape, generator=g).to(torch.bfloat16))
+    graph.replay()
+    torch.cuda.synchronize()
+    got = bits(outs)
+    ref2 = bits(fwd())
+    assert all(torch.equal(a, b) for a, b in zip(got, ref2)), "replay on new inputs differs from the eager call"
+    assert not torch.equal(ref2[0], ref[0])
+
+
 @pytest.mark.parametrize("pre_rope", [True, False])
 def test_block_cache_only_forward(pre_rope):
     """kv_cache_write_only (dit.py:446-459): img / txt come back unchanged; the first
