@@ -903,27 +903,22 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4q(
     }
   };
 
-  // prologue: steps 0 and 1 of the first tile
+  // prologue: steps 0 and 1 of the first tile, both landed before the first step (whose wait then
+  // counts the same outstanding operations as on every later tile)
   issue(0, 0);
   issue(1, KS);
-  wait_vmcnt<LOADS>();
+  wait_vmcnt<0>();
   block_barrier();
-  bool first = true;
   for (;;) {
     // the first step's A fragments and W fragments [0, FH) (slot 0: landed before the last barrier)
 #pragma unroll
     for (int f = 0; f < FM; ++f) fa[f] = frag(lds + a_row0 + f * 16 * KS);
 #pragma unroll
     for (int f = 0; f < FH; ++f) fw[f] = frag(lds + w_row0 + f * 16 * KS);
-    // step 0: its wait is for step 1, issued before the previous tile's NST epilogue stores
-    if (first) {
-      step(IC<0>{}, T_{}, IC<0>{}, true, 2 * KS, T_{});
-    } else {
-      // the fused QKV epilogue issues 2 NST stores (and, on q / k tiles, table loads that it has
-      // waited for) after step 1's last DMA: up to 63 of them may still be in flight
-      step(IC<0>{}, T_{}, IC<kEpi == kEpiQkv ? 63 : NST>{}, true, 2 * KS, T_{});
-    }
-    first = false;
+    // step 0: its wait is for step 1, issued before the previous tile's NST epilogue stores (the
+    // fused QKV epilogue issues 2 NST stores, and on q / k tiles table loads that it has waited for,
+    // after step 1's last DMA: up to 63 of them may still be in flight)
+    step(IC<0>{}, T_{}, IC<kEpi == kEpiQkv ? 63 : NST>{}, true, 2 * KS, T_{});
     step(IC<1>{}, F{}, IC<0>{}, false, 3 * KS, T_{});
     for (int kt = 2; kt + 2 < nk; kt += 2) {
       step(IC<0>{}, F{}, IC<0>{}, false, (kt + 2) * KS, T_{});
