@@ -985,7 +985,9 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4q(
         // chunk ahead (vmcnt is in order: loads issued after the previous chunk's stores would wait
         // for them too), then passed through the staging area (rows of 136 bytes: the lanes' 4-byte
         // reads of one pair column hit distinct banks) to the lanes that rotate each pair
-        u32x4 tb[4], tbn[4];
+        // zeroed, so that the v tiles (which load no tables) carry no values across tiles: left
+        // undefined, 32 registers of them were spilled around every tile's K loop
+        u32x4 tb[4] = {}, tbn[4] = {};
         auto load_tables = [&](int j, u32x4 (&t)[4]) {
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
